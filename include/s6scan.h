@@ -1,0 +1,147 @@
+/*
+ * s6scan -- MI355X (gfx950) S6 selective scan, C ABI.
+ *
+ * This is the native boundary below the reference's Python autograd op
+ * ``SelectiveScanFn`` (/root/reference/zoology/zoology/mixers/mamba_ssm/ops/
+ * selective_scan_interface.py:19-88).  The reference binds an un-vendored pybind module
+ * ``selective_scan_cuda`` with
+ *     fwd(u, delta, A, B, C, D, z, delta_bias, delta_softplus) -> (out, x, [out_z])
+ *         (selective_scan_interface.py:42, 225-227)
+ *     bwd(u, delta, A, B, C, D, z, delta_bias, dout, x, out, dz, delta_softplus,
+ *         recompute_out_z) -> (du, ddelta, dA, dB, dC, dD, ddelta_bias, [dz, [out_z]])
+ *         (selective_scan_interface.py:67-70, 263-267)
+ * s6_fwd / s6_bwd replace those two calls.  The arguments carry the same tensors as
+ * plain device pointers plus element strides; the caller allocates every tensor
+ * (outputs and workspace included) and the library never allocates device memory.
+ *
+ * Conventions
+ *   u, delta, z, out, out_z, dout, du, ddelta, dz : [batch, dim, seqlen], any strides
+ *   A                                              : [dim, dstate] fp32, any strides
+ *   B, C, dB, dC                                   : [batch, ngroups, dstate, seqlen], any strides
+ *   D, delta_bias, dD, ddelta_bias                 : [dim] fp32, any stride
+ *   x_ckpt                                         : [batch, dim, s6_num_checkpoints(), dstate] fp32,
+ *                                                    contiguous; entry k is the state after
+ *                                                    step min((k+1)*S6_CKPT_INTERVAL, seqlen)-1,
+ *                                                    so entry [-1] is the final state.
+ *   last_state                                     : [batch, dim, dstate] fp32 contiguous
+ *                                                    ([nseq, dim, dstate] for varlen)
+ *   Varlen (nseq > 0): batch == 1, cu_seqlens is a device int32 [nseq+1] with
+ *   cu_seqlens[0] == 0, non-decreasing, cu_seqlens[nseq] == seqlen; the state is reset to
+ *   zero at every sequence start (the seq_idx convention of the reference's chunked scans,
+ *   ssd_state_passing.py:76-78).
+ *
+ * Errors: every entry point returns S6_OK (0) or a negative S6_E* code; the message of the
+ * last failure on the calling thread is returned by s6_last_error().
+ * Streams: all device work is enqueued on the given hipStream_t (NULL = default stream),
+ * asynchronously; the library keeps no pointers after return and holds no global
+ * device state, so calls on different streams with different workspaces may overlap.
+ */
+#ifndef S6SCAN_H
+#define S6SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S6_ABI_VERSION 1
+#define S6_CKPT_INTERVAL 32   /* steps between saved states in x_ckpt */
+#define S6_MAX_DSTATE_FWD 64
+#define S6_MAX_DSTATE_BWD 16
+
+enum s6_dtype { S6_F32 = 0, S6_BF16 = 1, S6_F16 = 2 };
+
+enum s6_status {
+  S6_OK = 0,
+  S6_E_INVALID = -1,      /* bad argument: shape, stride, dtype, null pointer */
+  S6_E_UNSUPPORTED = -2,  /* valid in the reference but not provided by this library */
+  S6_E_WORKSPACE = -3,    /* workspace missing or too small */
+  S6_E_HIP = -4           /* a HIP runtime call failed */
+};
+
+typedef struct S6Problem {
+  int64_t batch, dim, seqlen, dstate, ngroups;
+  int32_t io_dtype;        /* u, delta, z, out, out_z, dout, du, ddelta, dz */
+  int32_t bc_dtype;        /* B, C (dB, dC are always fp32) */
+  int32_t has_D, has_z, has_delta_bias, delta_softplus;
+  int32_t nseq;            /* 0: dense batch; > 0: packed varlen, batch must be 1 */
+} S6Problem;
+
+typedef struct S6FwdArgs {
+  S6Problem p;
+  const void* u;            int64_t u_stride[3];
+  const void* delta;        int64_t delta_stride[3];
+  const float* A;           int64_t A_stride[2];
+  const void* B;            int64_t B_stride[4];
+  const void* C;            int64_t C_stride[4];
+  const float* D;           int64_t D_stride;
+  const void* z;            int64_t z_stride[3];
+  const float* delta_bias;  int64_t delta_bias_stride;
+  const int32_t* cu_seqlens;
+  void* out;                int64_t out_stride[3];    /* y + D*u (before the z gate)     */
+  void* out_z;              int64_t out_z_stride[3];  /* out * silu(z); has_z only       */
+  float* x_ckpt;            /* may be NULL (no backward will follow)                    */
+  float* last_state;        /* may be NULL                                               */
+  void* workspace;          size_t workspace_bytes;
+} S6FwdArgs;
+
+typedef struct S6BwdArgs {
+  S6Problem p;
+  const void* u;            int64_t u_stride[3];
+  const void* delta;        int64_t delta_stride[3];
+  const float* A;           int64_t A_stride[2];
+  const void* B;            int64_t B_stride[4];
+  const void* C;            int64_t C_stride[4];
+  const float* D;           int64_t D_stride;
+  const void* z;            int64_t z_stride[3];
+  const float* delta_bias;  int64_t delta_bias_stride;
+  const int32_t* cu_seqlens;
+  const void* dout;         int64_t dout_stride[3];
+  const float* x_ckpt;      /* as written by s6_fwd for the same inputs                  */
+  const void* out;          int64_t out_stride[3];    /* pre-gate output; has_z only    */
+  void* du;                 int64_t du_stride[3];
+  void* ddelta;             int64_t ddelta_stride[3];
+  float* dA;                int64_t dA_stride[2];
+  float* dB;                int64_t dB_stride[4];
+  float* dC;                int64_t dC_stride[4];
+  float* dD;                int64_t dD_stride;        /* has_D only                     */
+  void* dz;                 int64_t dz_stride[3];     /* has_z only                     */
+  float* ddelta_bias;       int64_t ddelta_bias_stride; /* has_delta_bias only          */
+  void* workspace;          size_t workspace_bytes;
+} S6BwdArgs;
+
+/* ABI version of the loaded library (S6_ABI_VERSION it was built with). */
+int s6_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* s6_last_error(void);
+
+/* Host-only shape/dtype check of a problem (no device access). */
+int s6_validate_problem(const S6Problem* p);
+
+/* Host-only check of forward / backward arguments (shapes, strides, null pointers,
+ * workspace size).  s6_fwd / s6_bwd run the same checks before launching. */
+int s6_validate_fwd(const S6FwdArgs* a);
+int s6_validate_bwd(const S6BwdArgs* a);
+
+/* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */
+int64_t s6_num_checkpoints(const S6Problem* p);
+
+/* Device workspace the calls need, in bytes (0 is possible). */
+size_t s6_fwd_workspace_bytes(const S6Problem* p);
+size_t s6_bwd_workspace_bytes(const S6Problem* p);
+
+/* Forward scan: replaces selective_scan_cuda.fwd (selective_scan_interface.py:42). */
+int s6_fwd(const S6FwdArgs* a, void* stream);
+
+/* Backward scan: replaces selective_scan_cuda.bwd (selective_scan_interface.py:67-70).
+ * dA, dB, dC, dD, ddelta_bias are overwritten (not accumulated into). */
+int s6_bwd(const S6BwdArgs* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* S6SCAN_H */

@@ -1,0 +1,374 @@
+// C ABI of the S6 selective-scan library: argument validation, workspace planning and
+// kernel dispatch.  Validation and planning are host-only and never touch a device, so
+// they can be exercised (and are, by the CPU tests) on a machine without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "s6_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return S6_OK;
+}
+
+constexpr int64_t kTargetWaves = 4096;  // 16 waves per CU on a 256-CU MI355X
+constexpr int64_t kMinChunk = 128;
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+int esize(int dt) { return dt == S6_F32 ? 4 : 2; }
+
+struct Plan {
+  int64_t Dg, nJ64, nJ256, nDblk64;
+  int64_t K, Lc, nck;
+  bool relayout_B, relayout_C;
+  int64_t NP;  // padded dstate of relaid-out B / C
+  size_t off_h, off_s, off_B, off_C, off_pB, off_pC, total_fwd, total_bwd;
+};
+
+// States held per lane by the kernels: the forward pads dstate to 8/16/32/64, the backward
+// to 16.  B and C rows are read as NS contiguous values, so a row is used in place only
+// when dstate == NS, the state axis is contiguous and 16-bit rows are 4-byte aligned.
+int64_t ns_fwd(int64_t N) { return N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
+int64_t ns_bwd(int64_t) { return 16; }
+
+bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_t NS) {
+  if (N != NS || s[2] != 1) return false;
+  if (dt == S6_F32) return true;
+  if (((uintptr_t)ptr & 3u) != 0) return false;
+  if ((N & 1) != 0) return false;
+  return (s[0] % 2 == 0) && (s[1] % 2 == 0) && (s[3] % 2 == 0);
+}
+
+// Chunking and workspace layout; ptrs may be null (sizing only, then relayout is assumed
+// to be needed exactly when the strides say so).
+Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, const void* Cp,
+               const int64_t* sC) {
+  Plan pl{};
+  pl.Dg = p.dim / p.ngroups;
+  pl.nJ64 = ceil_div(pl.Dg, 64);
+  pl.nJ256 = ceil_div(pl.Dg, 256);
+  pl.nDblk64 = p.ngroups * pl.nJ64;
+  const int64_t chw = p.batch * pl.nDblk64;
+  const int64_t ktarget = ceil_div(kTargetWaves, chw > 0 ? chw : 1);
+  int64_t Lc = ceil_div(p.seqlen, ktarget > 0 ? ktarget : 1);
+  if (Lc < kMinChunk) Lc = kMinChunk;
+  Lc = ceil_div(Lc, s6::kCk) * s6::kCk;
+  pl.Lc = Lc;
+  pl.K = ceil_div(p.seqlen, Lc);
+  pl.nck = ceil_div(p.seqlen, s6::kCk);
+  const int64_t NS = bwd ? ns_bwd(p.dstate) : ns_fwd(p.dstate);
+  // Without pointers (sizing queries) assume the worst case: both B and C relaid out.
+  pl.relayout_B = sB ? !bc_scalar_ok(Bp, sB, p.bc_dtype, p.dstate, NS) : true;
+  pl.relayout_C = sC ? !bc_scalar_ok(Cp, sC, p.bc_dtype, p.dstate, NS) : true;
+  pl.NP = NS;
+  const size_t nchan = (size_t)(p.batch * p.dim);
+  size_t off = 0;
+  pl.off_h = off;
+  off += pl.K > 1 ? align256(nchan * pl.K * p.dstate * 4) : 0;
+  pl.off_s = off;
+  off += pl.K > 1 ? align256(nchan * pl.K * 4) : 0;
+  const size_t bc_bytes = align256((size_t)(p.batch * p.ngroups * p.seqlen * pl.NP) * esize(p.bc_dtype));
+  pl.off_B = off;
+  off += pl.relayout_B ? bc_bytes : 0;
+  pl.off_C = off;
+  off += pl.relayout_C ? bc_bytes : 0;
+  pl.total_fwd = off;
+  const size_t part = align256((size_t)(p.batch * p.ngroups * pl.nJ256 * p.seqlen * p.dstate) * 4);
+  pl.off_pB = off;
+  off += part;
+  pl.off_pC = off;
+  off += part;
+  pl.total_bwd = off;
+  return pl;
+}
+
+int check_ptr(const void* p, const char* name) {
+  if (p == nullptr) return fail(S6_E_INVALID, "%s must not be NULL", name);
+  return S6_OK;
+}
+
+int check_strides(const int64_t* s, int n, const char* name) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] < 0) return fail(S6_E_INVALID, "%s has a negative stride", name);
+  return S6_OK;
+}
+
+int check_common(const S6Problem& p, const void* u, const int64_t* su, const void* delta,
+                 const int64_t* sdl, const float* A, const int64_t* sA, const void* B,
+                 const int64_t* sB, const void* C, const int64_t* sC, const float* D,
+                 const void* z, const int64_t* sz, const float* bias, const int32_t* cu) {
+  int r;
+  if ((r = s6_validate_problem(&p)) != S6_OK) return r;
+  if ((r = check_ptr(u, "u")) || (r = check_ptr(delta, "delta")) || (r = check_ptr(A, "A")) ||
+      (r = check_ptr(B, "B")) || (r = check_ptr(C, "C")))
+    return r;
+  if ((r = check_strides(su, 3, "u")) || (r = check_strides(sdl, 3, "delta")) ||
+      (r = check_strides(sA, 2, "A")) || (r = check_strides(sB, 4, "B")) ||
+      (r = check_strides(sC, 4, "C")))
+    return r;
+  if (p.has_D && (r = check_ptr(D, "D"))) return r;
+  if (p.has_z) {
+    if ((r = check_ptr(z, "z"))) return r;
+    if ((r = check_strides(sz, 3, "z"))) return r;
+  }
+  if (p.has_delta_bias && (r = check_ptr(bias, "delta_bias"))) return r;
+  if (p.nseq > 0 && (r = check_ptr(cu, "cu_seqlens"))) return r;
+  return S6_OK;
+}
+
+s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
+  s6::FwdK k{};
+  const S6Problem& p = a.p;
+  k.Bsz = p.batch; k.D = p.dim; k.L = p.seqlen; k.N = p.dstate; k.G = p.ngroups;
+  for (int i = 0; i < 3; ++i) {
+    k.su[i] = a.u_stride[i]; k.sdl[i] = a.delta_stride[i];
+    k.sz[i] = p.has_z ? a.z_stride[i] : 0;
+    k.so[i] = a.out_stride[i];
+    k.soz[i] = p.has_z ? a.out_z_stride[i] : 0;
+  }
+  k.sA[0] = a.A_stride[0]; k.sA[1] = a.A_stride[1];
+  k.sD = a.D_stride; k.sbias = a.delta_bias_stride;
+  k.u = a.u; k.delta = a.delta; k.z = a.z; k.A = a.A; k.Dp = a.D; k.bias = a.delta_bias;
+  char* ws = (char*)a.workspace;
+  const int64_t NP = pl.NP;
+  if (pl.relayout_B) {
+    k.Bm = ws + pl.off_B;
+    k.sB[0] = p.ngroups * p.seqlen * NP; k.sB[1] = p.seqlen * NP; k.sB[2] = 1; k.sB[3] = NP;
+  } else {
+    k.Bm = a.B;
+    for (int i = 0; i < 4; ++i) k.sB[i] = a.B_stride[i];
+  }
+  if (pl.relayout_C) {
+    k.Cm = ws + pl.off_C;
+    k.sC[0] = p.ngroups * p.seqlen * NP; k.sC[1] = p.seqlen * NP; k.sC[2] = 1; k.sC[3] = NP;
+  } else {
+    k.Cm = a.C;
+    for (int i = 0; i < 4; ++i) k.sC[i] = a.C_stride[i];
+  }
+  k.cu = a.cu_seqlens; k.nseq = p.nseq;
+  k.out = a.out; k.out_z = a.out_z;
+  k.x_ckpt = a.x_ckpt; k.nck = pl.nck; k.last_state = a.last_state;
+  k.ws_h = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
+  k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;
+  k.ws_r = nullptr;
+  k.K = pl.K; k.Lc = pl.Lc;
+  k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
+  k.nDblk = pl.nDblk64;
+  return k;
+}
+
+}  // namespace
+
+extern "C" {
+
+int s6_abi_version(void) { return S6_ABI_VERSION; }
+
+const char* s6_last_error(void) { return g_last_error.c_str(); }
+
+int s6_validate_problem(const S6Problem* p) {
+  if (p == nullptr) return fail(S6_E_INVALID, "problem must not be NULL");
+  if (p->batch < 1 || p->dim < 1 || p->seqlen < 1 || p->dstate < 1 || p->ngroups < 1)
+    return fail(S6_E_INVALID,
+                "batch, dim, seqlen, dstate and ngroups must be >= 1 (got %lld, %lld, %lld, %lld, %lld)",
+                (long long)p->batch, (long long)p->dim, (long long)p->seqlen,
+                (long long)p->dstate, (long long)p->ngroups);
+  if (p->dim % p->ngroups != 0)
+    return fail(S6_E_INVALID, "dim (%lld) must be divisible by the number of B/C groups (%lld)",
+                (long long)p->dim, (long long)p->ngroups);
+  for (int dt : {p->io_dtype, p->bc_dtype})
+    if (dt != S6_F32 && dt != S6_BF16 && dt != S6_F16)
+      return fail(S6_E_INVALID, "unknown dtype code %d", dt);
+  if (p->dstate > S6_MAX_DSTATE_FWD)
+    return fail(S6_E_UNSUPPORTED, "dstate %lld exceeds the supported maximum %d",
+                (long long)p->dstate, S6_MAX_DSTATE_FWD);
+  if (p->nseq < 0) return fail(S6_E_INVALID, "nseq must be >= 0");
+  if (p->nseq > 0 && p->batch != 1)
+    return fail(S6_E_INVALID, "packed varlen input (cu_seqlens) requires batch == 1, got %lld",
+                (long long)p->batch);
+  if (p->seqlen > (int64_t)INT32_MAX)
+    return fail(S6_E_UNSUPPORTED, "seqlen must fit in int32 for cu_seqlens offsets");
+  return ok();
+}
+
+int64_t s6_num_checkpoints(const S6Problem* p) {
+  if (p == nullptr || p->seqlen < 1) return 0;
+  return ceil_div(p->seqlen, s6::kCk);
+}
+
+size_t s6_fwd_workspace_bytes(const S6Problem* p) {
+  if (s6_validate_problem(p) != S6_OK) return 0;
+  return make_plan(*p, false, nullptr, nullptr, nullptr, nullptr).total_fwd;
+}
+
+size_t s6_bwd_workspace_bytes(const S6Problem* p) {
+  if (s6_validate_problem(p) != S6_OK) return 0;
+  return make_plan(*p, true, nullptr, nullptr, nullptr, nullptr).total_bwd;
+}
+
+int s6_validate_fwd(const S6FwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  const S6Problem& p = a->p;
+  int r = check_common(p, a->u, a->u_stride, a->delta, a->delta_stride, a->A, a->A_stride,
+                       a->B, a->B_stride, a->C, a->C_stride, a->D, a->z, a->z_stride,
+                       a->delta_bias, a->cu_seqlens);
+  if (r != S6_OK) return r;
+  if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 3, "out"))) return r;
+  if (p.has_z && ((r = check_ptr(a->out_z, "out_z")) || (r = check_strides(a->out_z_stride, 3, "out_z"))))
+    return r;
+  const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
+  if (pl.total_fwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_fwd))
+    return fail(S6_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", pl.total_fwd,
+                a->workspace ? a->workspace_bytes : (size_t)0);
+  return ok();
+}
+
+int s6_validate_bwd(const S6BwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  const S6Problem& p = a->p;
+  int r = check_common(p, a->u, a->u_stride, a->delta, a->delta_stride, a->A, a->A_stride,
+                       a->B, a->B_stride, a->C, a->C_stride, a->D, a->z, a->z_stride,
+                       a->delta_bias, a->cu_seqlens);
+  if (r != S6_OK) return r;
+  if (p.dstate > S6_MAX_DSTATE_BWD)
+    return fail(S6_E_UNSUPPORTED, "backward supports dstate <= %d, got %lld", S6_MAX_DSTATE_BWD,
+                (long long)p.dstate);
+  if ((r = check_ptr(a->dout, "dout")) || (r = check_strides(a->dout_stride, 3, "dout")) ||
+      (r = check_ptr(a->x_ckpt, "x_ckpt")) || (r = check_ptr(a->du, "du")) ||
+      (r = check_strides(a->du_stride, 3, "du")) || (r = check_ptr(a->ddelta, "ddelta")) ||
+      (r = check_strides(a->ddelta_stride, 3, "ddelta")) || (r = check_ptr(a->dA, "dA")) ||
+      (r = check_strides(a->dA_stride, 2, "dA")) || (r = check_ptr(a->dB, "dB")) ||
+      (r = check_strides(a->dB_stride, 4, "dB")) || (r = check_ptr(a->dC, "dC")) ||
+      (r = check_strides(a->dC_stride, 4, "dC")))
+    return r;
+  if (p.has_D && (r = check_ptr(a->dD, "dD"))) return r;
+  if (p.has_z && ((r = check_ptr(a->dz, "dz")) || (r = check_strides(a->dz_stride, 3, "dz")) ||
+                  (r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 3, "out"))))
+    return r;
+  if (p.has_delta_bias && (r = check_ptr(a->ddelta_bias, "ddelta_bias"))) return r;
+  const Plan pl = make_plan(p, true, a->B, a->B_stride, a->C, a->C_stride);
+  if (pl.total_bwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_bwd))
+    return fail(S6_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", pl.total_bwd,
+                a->workspace ? a->workspace_bytes : (size_t)0);
+  return ok();
+}
+
+int s6_fwd(const S6FwdArgs* a, void* stream) {
+  int r = s6_validate_fwd(a);
+  if (r != S6_OK) return r;
+  const S6Problem& p = a->p;
+  hipStream_t st = (hipStream_t)stream;
+  const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
+  char* ws = (char*)a->workspace;
+  hipError_t e = hipSuccess;
+  if (pl.relayout_B)
+    e = s6::launch_relayout(a->B, a->B_stride, esize(p.bc_dtype), ws + pl.off_B, p.batch,
+                            p.ngroups, p.dstate, pl.NP, p.seqlen, st);
+  if (e == hipSuccess && pl.relayout_C)
+    e = s6::launch_relayout(a->C, a->C_stride, esize(p.bc_dtype), ws + pl.off_C, p.batch,
+                            p.ngroups, p.dstate, pl.NP, p.seqlen, st);
+  if (e == hipSuccess && a->last_state != nullptr && p.nseq > 0)
+    e = s6::launch_fill(a->last_state, (int64_t)p.nseq * p.dim * p.dstate, 0.f, st);
+  if (e == hipSuccess) {
+    s6::FwdK k = fill_fwd(*a, pl);
+    e = s6::launch_fwd(k, p.io_dtype, p.bc_dtype, st);
+  }
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_fwd: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int s6_bwd(const S6BwdArgs* a, void* stream) {
+  int r = s6_validate_bwd(a);
+  if (r != S6_OK) return r;
+  const S6Problem& p = a->p;
+  hipStream_t st = (hipStream_t)stream;
+  const Plan pl = make_plan(p, true, a->B, a->B_stride, a->C, a->C_stride);
+  char* ws = (char*)a->workspace;
+  hipError_t e = hipSuccess;
+  if (pl.relayout_B)
+    e = s6::launch_relayout(a->B, a->B_stride, esize(p.bc_dtype), ws + pl.off_B, p.batch,
+                            p.ngroups, p.dstate, pl.NP, p.seqlen, st);
+  if (e == hipSuccess && pl.relayout_C)
+    e = s6::launch_relayout(a->C, a->C_stride, esize(p.bc_dtype), ws + pl.off_C, p.batch,
+                            p.ngroups, p.dstate, pl.NP, p.seqlen, st);
+  // dA, dD and ddelta_bias are accumulated with atomics: clear them first (fill kernels,
+  // not memset nodes, so the sequence stays valid inside a captured graph).
+  if (e == hipSuccess && a->dA_stride[1] == 1 && a->dA_stride[0] == p.dstate)
+    e = s6::launch_fill(a->dA, p.dim * p.dstate, 0.f, st);
+  else if (e == hipSuccess)
+    return fail(S6_E_INVALID, "dA must be a contiguous [dim, dstate] fp32 tensor");
+  if (e == hipSuccess && p.has_D) {
+    if (a->dD_stride != 1) return fail(S6_E_INVALID, "dD must be contiguous");
+    e = s6::launch_fill(a->dD, p.dim, 0.f, st);
+  }
+  if (e == hipSuccess && p.has_delta_bias) {
+    if (a->ddelta_bias_stride != 1) return fail(S6_E_INVALID, "ddelta_bias must be contiguous");
+    e = s6::launch_fill(a->ddelta_bias, p.dim, 0.f, st);
+  }
+  if (e == hipSuccess) {
+    s6::BwdK k{};
+    k.Bsz = p.batch; k.D = p.dim; k.L = p.seqlen; k.N = p.dstate; k.G = p.ngroups;
+    for (int i = 0; i < 3; ++i) {
+      k.su[i] = a->u_stride[i]; k.sdl[i] = a->delta_stride[i];
+      k.sz[i] = p.has_z ? a->z_stride[i] : 0;
+      k.sdo[i] = a->dout_stride[i];
+      k.sout[i] = p.has_z ? a->out_stride[i] : 0;
+      k.sdu[i] = a->du_stride[i]; k.sddl[i] = a->ddelta_stride[i];
+      k.sdz[i] = p.has_z ? a->dz_stride[i] : 0;
+    }
+    k.sA[0] = a->A_stride[0]; k.sA[1] = a->A_stride[1];
+    k.sD = a->D_stride; k.sbias = a->delta_bias_stride;
+    const int64_t NP = pl.NP;
+    if (pl.relayout_B) {
+      k.Bm = ws + pl.off_B;
+      k.sB[0] = p.ngroups * p.seqlen * NP; k.sB[1] = p.seqlen * NP; k.sB[2] = 1; k.sB[3] = NP;
+    } else {
+      k.Bm = a->B;
+      for (int i = 0; i < 4; ++i) k.sB[i] = a->B_stride[i];
+    }
+    if (pl.relayout_C) {
+      k.Cm = ws + pl.off_C;
+      k.sC[0] = p.ngroups * p.seqlen * NP; k.sC[1] = p.seqlen * NP; k.sC[2] = 1; k.sC[3] = NP;
+    } else {
+      k.Cm = a->C;
+      for (int i = 0; i < 4; ++i) k.sC[i] = a->C_stride[i];
+    }
+    k.sdA[0] = a->dA_stride[0]; k.sdA[1] = a->dA_stride[1];
+    k.sdD = a->dD_stride; k.sdbias = a->ddelta_bias_stride;
+    for (int i = 0; i < 4; ++i) { k.sdB[i] = a->dB_stride[i]; k.sdC[i] = a->dC_stride[i]; }
+    k.u = a->u; k.delta = a->delta; k.z = a->z; k.dout = a->dout; k.out = a->out;
+    k.A = a->A; k.Dp = a->D; k.bias = a->delta_bias;
+    k.cu = a->cu_seqlens; k.nseq = p.nseq;
+    k.x_ckpt = a->x_ckpt; k.nck = pl.nck;
+    k.du = a->du; k.ddelta = a->ddelta; k.dz = a->dz;
+    k.dA = a->dA; k.dD = a->dD; k.dbias = a->ddelta_bias; k.dB = a->dB; k.dC = a->dC;
+    k.ws_g = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
+    k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;
+    k.ws_pB = (float*)(ws + pl.off_pB);
+    k.ws_pC = (float*)(ws + pl.off_pC);
+    k.K = pl.K; k.Lc = pl.Lc;
+    k.nDblk = pl.nDblk64; k.nJ4 = pl.nJ256;
+    k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
+    e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st);
+  }
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_bwd: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// Shared definitions for the gfx950 S6 selective-scan kernels (device side and host side).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "s6scan.h"
+
+namespace s6 {
+
+constexpr int kWave = 64;            // CDNA wavefront width
+constexpr int kCk = S6_CKPT_INTERVAL;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Element storage types (tags; raw bits for the 16-bit formats).
+struct bf16 { uint16_t bits; };
+struct f16 { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kSize = 4;
+  __device__ static inline float load(const void* p, int64_t i) {
+    return reinterpret_cast<const float*>(p)[i];
+  }
+  __device__ static inline void store(void* p, int64_t i, float v) {
+    reinterpret_cast<float*>(p)[i] = v;
+  }
+};
+template <> struct Elem<bf16> {
+  static constexpr int kSize = 2;
+  __device__ static inline float load(const void* p, int64_t i) {
+    uint32_t b = reinterpret_cast<const uint16_t*>(p)[i];
+    return __uint_as_float(b << 16);
+  }
+  __device__ static inline void store(void* p, int64_t i, float v) {
+    // gfx950 converts f32 -> bf16 with round-to-nearest-even in hardware.
+    __bf16 h = static_cast<__bf16>(v);
+    reinterpret_cast<__bf16*>(p)[i] = h;
+  }
+};
+template <> struct Elem<f16> {
+  static constexpr int kSize = 2;
+  __device__ static inline float load(const void* p, int64_t i) {
+    return static_cast<float>(reinterpret_cast<const _Float16*>(p)[i]);
+  }
+  __device__ static inline void store(void* p, int64_t i, float v) {
+    reinterpret_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+  }
+};
+
+// Uniform (wave-invariant) loads of B_t / C_t through the scalar cache.  The pointer is
+// cast to the constant address space so a uniform address is selected as s_load; the
+// 16-bit formats are loaded as packed 32-bit pairs and unpacked on the scalar unit.
+typedef const __attribute__((address_space(4))) uint32_t* cu32p;
+
+template <typename T> struct BCLoad;
+template <> struct BCLoad<float> {
+  // row points at element n=0 of a time step; the row holds NS valid (or zero-padded) values.
+  template <int NS>
+  __device__ static inline void row(const void* row, float (&v)[NS]) {
+    cu32p r = (cu32p)row;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) v[n] = __uint_as_float(r[n]);
+  }
+};
+template <> struct BCLoad<bf16> {
+  template <int NS>
+  __device__ static inline void row(const void* row, float (&v)[NS]) {
+    cu32p r = (cu32p)row;
+#pragma unroll
+    for (int n = 0; n < NS; n += 2) {
+      const uint32_t w = r[n / 2];
+      v[n] = __uint_as_float(w << 16);
+      v[n + 1] = __uint_as_float(w & 0xffff0000u);
+    }
+  }
+};
+template <> struct BCLoad<f16> {
+  template <int NS>
+  __device__ static inline void row(const void* row, float (&v)[NS]) {
+    cu32p r = (cu32p)row;
+#pragma unroll
+    for (int n = 0; n < NS; n += 2) {
+      const uint32_t w = r[n / 2];
+      v[n] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+      v[n + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+  }
+};
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// F.softplus with beta=1, threshold=20 (selective_scan_interface.py:111-112).
+__device__ inline float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
+// d softplus / dx, matching torch's softplus_backward (exp(x)/(exp(x)+1) below threshold).
+__device__ inline float softplus20_grad(float x) {
+  if (x > 20.f) return 1.f;
+  float e = expf(x);
+  return e / (e + 1.f);
+}
+__device__ inline float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Kernel parameter block shared by the forward kernels (plain values; strides in elements).
+struct FwdK {
+  int64_t Bsz, D, L, N, G;
+  int64_t su[3], sdl[3], sz[3], so[3], soz[3];
+  int64_t sA[2], sD, sbias;
+  int64_t sB[4], sC[4];  // B/C strides; sB[2] (n) == 1 for the scalar path
+  const void* u; const void* delta; const void* z;
+  const float* A; const float* Dp; const float* bias;
+  const void* Bm; const void* Cm;
+  const int32_t* cu; int32_t nseq;
+  void* out; void* out_z;
+  float* x_ckpt; int64_t nck;
+  float* last_state;
+  float* ws_h;    // [Bsz*D, K, N]  chunk summaries, then carried-in states
+  float* ws_s;    // [Bsz*D, K]     sum of Delta since the last reset in the chunk
+  int32_t* ws_r;  // [K]            1 if a sequence starts inside the chunk
+  int64_t K, Lc;  // number of chunks and chunk length (multiple of kCk)
+  int32_t has_D, has_z, has_bias, softplus;
+  int64_t nDblk;  // ceil(D / 64)
+};
+
+}  // namespace s6
