@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X S6 selective scan; prints ONE JSON line on stdout.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwd1|fwdbwd3|fwd2|fwdbwd4]
+
+Default workload ``fwd1``: the forward scan at B=32, L=4096, D=256, N=16, bf16 I/O with
+fp32 state (the configuration the headline metric is quoted on), called like a [B, L, D]
+producer would: ``selective_scan_fn(x.mT, delta.mT, A, B.mT, C.mT, D=D,
+return_last_state=True)``.  ``fwdbwd3`` times forward + backward at B=8, L=8192, D=768,
+N=16 bf16; ``fwd2`` the fp32 N=64 long-sequence forward; ``fwdbwd4`` the packed varlen
+forward + backward.
+
+* value: algorithmic HBM bytes of one step (each tensor once) / wall time per step, with
+  the inputs resident in HBM.  Three independent input sets rotate so the 256 MB
+  Infinity Cache cannot hold the working set.
+* roofline: the dominant kernel (the fused scan/output kernel) timed live with HIP events
+  that the library records on its own stream around that kernel.
+* cpu_baseline: the CPU restatement of the reference path (selective_scan_ref, op for op,
+  oracle/selective_scan_ref.py) timed on the host cores on a bounded sample of the same
+  workload.
+Only one GPU is used: --gpus above 1 exits with a message.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ml-experiments_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "scan fwd / fwd+bwd achieved HBM GB/s (% of peak) and Mtok·ch/s at 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="fwd1", choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, make_inputs):
+    """Reference CPU path (torch restatement of selective_scan_ref) on a bounded sample:
+    one sequence of the workload (4096 steps forward, 2048 steps forward + backward)."""
+    import dataclasses
+
+    import torch
+    from oracle.selective_scan_ref import selective_scan_ref, selective_scan_ref_grads
+    torch.set_num_threads(os.cpu_count() or 1)
+    seqlen = 2048 if (cfg.backward or not cfg.seqlen) else min(cfg.seqlen, 4096)
+    sample = dataclasses.replace(cfg, batch=1, seqlen=seqlen, nseq=0)
+    inp = make_inputs(sample)
+    args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
+
+    def run():
+        if sample.backward:
+            selective_scan_ref_grads(*args, inp["D"], inp["dy"].mT)
+        else:
+            selective_scan_ref(*args, D=inp["D"], return_last_state=True)
+
+    run()  # warm-up
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t)
+    sec = statistics.median(ts)
+    return {
+        "value": round(sample.algorithmic_bytes() / sec / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"restated reference CPU path (selective_scan_ref op for op"
+                   f"{' + autograd backward' if sample.backward else ''}) on one sequence of "
+                   f"{cfg.name}: batch 1, seqlen {seqlen}, dim {cfg.dim}, dstate {cfg.dstate}; "
+                   f"median of 3 runs = {sec:.3f} s; os.cpu_count() = {os.cpu_count()}"),
+        "mtok_ch_per_s": round(seqlen * cfg.dim / sec / 1e6, 4),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); the scan shards over batch/channels without "
+              "communication, so run it per GPU.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import s6scan
+    from s6scan.configs import CONFIGS, make_inputs
+    from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
+
+    cfg = {"fwd1": CONFIGS[1], "fwdbwd3": CONFIGS[3], "fwd2": CONFIGS[2],
+           "fwdbwd4": CONFIGS[4]}[args.workload]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    # Three independent input sets (rotated every step) exceed the 256 MB Infinity Cache.
+    nsets = 3
+    sets = []
+    import dataclasses
+    for s in range(nsets):
+        cpu = make_inputs(dataclasses.replace(cfg, seed=cfg.seed + 1000 * s))
+        sets.append({k: v.to(dev) for k, v in cpu.items()})
+        del cpu
+    L = sets[0]["x"].shape[1]
+    B = sets[0]["x"].shape[0]
+    nbytes = cfg.algorithmic_bytes(seqlen=L)
+
+    def step(i, ev=None, ev_b=None):
+        g = sets[i % nsets]
+        a = (g["x"].mT, g["delta"].mT, g["A"], g["B"].mT, g["C"].mT)
+        cu = g.get("cu_seqlens")
+        if not cfg.backward:
+            with torch.no_grad():
+                selective_scan_forward(*a, D=g["D"], cu_seqlens=cu, want_ckpt=False,
+                                       want_last_state=True, kernel_events=ev)
+        else:
+            out, _, xck, _ = selective_scan_forward(*a, D=g["D"], cu_seqlens=cu, want_ckpt=True,
+                                                    want_last_state=True, kernel_events=ev)
+            selective_scan_backward(*a, g["D"], None, None, False, g["dy"].mT, xck, cu_seqlens=cu,
+                                    kernel_events=ev_b)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    evs = [(mk(), mk()) for _ in range(K)]
+    evs_b = [(mk(), mk()) for _ in range(K)] if cfg.backward else [None] * K
+    stream = torch.cuda.current_stream()
+    for pair in evs + [p for p in evs_b if p is not None]:
+        for e in pair:
+            e.record(stream)  # creates the underlying hipEvent_t; re-recorded by the library
+    g0, g1 = mk(), mk()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    g0.record(stream)
+    for i in range(K):
+        step(i, evs[i], evs_b[i])
+    g1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    ms_step = wall * 1e3 / K
+    gpu_ms_step = g0.elapsed_time(g1) / K
+    k_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    kb_ms = statistics.mean(a.elapsed_time(b) for a, b in evs_b) if cfg.backward else None
+
+    value = nbytes / (ms_step * 1e-3) / 1e9
+    fwd_bytes = cfg.algorithmic_bytes(seqlen=L, with_backward=False)
+    # Dominant kernel: the scan/output pass of the forward (backward main kernel for the
+    # fwd+bwd workloads); one launch processes every (token, channel) of the call.
+    if cfg.backward:
+        dom_name, dom_ms, dom_bytes = "bwd_main", kb_ms, nbytes - fwd_bytes
+    else:
+        dom_name, dom_ms, dom_bytes = "fwd_scan (output pass)", k_ms, fwd_bytes
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get(args.workload)
+    res = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "io_dtype": str(cfg.dtype).replace("torch.", ""),
+        "data": "synthetic (seeded normal/uniform inputs of the workload's shape; 3 rotating sets)",
+        "config": {"workload": f"{cfg.name}: selective_scan_fn {'fwd+bwd' if cfg.backward else 'fwd'}"
+                               " on channel-last [B, L, D] views",
+                   "batch": B, "seqlen": L, "dim": cfg.dim, "dstate": cfg.dstate,
+                   "nseq": cfg.nseq, "algorithmic_bytes_per_step": nbytes},
+        "hbm_frac": round(value / HBM_PEAK_GBS, 5),
+        "mtok_ch_per_s": round(B * L * cfg.dim / (ms_step * 1e-3) / 1e6, 2),
+        "gpu_event_ms_per_step": round(gpu_ms_step, 5),
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": round(achieved, 3),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic": traffic,
+            "kernel_ms": round(dom_ms, 5),
+        },
+    }
+    if cfg.backward:
+        res["fwd_kernel_ms"] = round(k_ms, 5)
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline(cfg, make_inputs)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

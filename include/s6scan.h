@@ -85,6 +85,10 @@ typedef struct S6FwdArgs {
   float* x_ckpt;            /* may be NULL (no backward will follow)                    */
   float* last_state;        /* may be NULL                                               */
   void* workspace;          size_t workspace_bytes;
+  /* Optional hipEvent_t pair (NULL = off), recorded on the call's stream right before and
+   * after the main scan kernel, so a caller can time that kernel alone.  No counterpart in
+   * the reference; it exists for roofline measurement. */
+  void* kernel_events[2];
 } S6FwdArgs;
 
 typedef struct S6BwdArgs {
@@ -110,6 +114,7 @@ typedef struct S6BwdArgs {
   void* dz;                 int64_t dz_stride[3];     /* has_z only                     */
   float* ddelta_bias;       int64_t ddelta_bias_stride; /* has_delta_bias only          */
   void* workspace;          size_t workspace_bytes;
+  void* kernel_events[2];   /* as in S6FwdArgs, around the main backward kernel          */
 } S6BwdArgs;
 
 /* ABI version of the loaded library (S6_ABI_VERSION it was built with). */

@@ -99,6 +99,18 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   return pl;
 }
 
+// The kernels address [batch, dim, seqlen] tensors through 32-bit buffer offsets relative
+// to a wave's first element: 63 channel strides plus one chunk of time strides must stay
+// below 2^31 bytes.
+int check_span(const int64_t* s, int es, int64_t Lc, const char* name) {
+  const int64_t span = (63 * s[1] + Lc * s[2]) * (int64_t)es;
+  if (span >= ((int64_t)1 << 31) - (1 << 20))
+    return fail(S6_E_UNSUPPORTED,
+                "%s: strides too large for 32-bit buffer offsets (63*%lld + %lld*%lld elements)",
+                name, (long long)s[1], (long long)Lc, (long long)s[2]);
+  return S6_OK;
+}
+
 int check_ptr(const void* p, const char* name) {
   if (p == nullptr) return fail(S6_E_INVALID, "%s must not be NULL", name);
   return S6_OK;
@@ -233,6 +245,11 @@ int s6_validate_fwd(const S6FwdArgs* a) {
   if (p.has_z && ((r = check_ptr(a->out_z, "out_z")) || (r = check_strides(a->out_z_stride, 3, "out_z"))))
     return r;
   const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
+  const int es = esize(p.io_dtype);
+  if ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
+      (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
+      (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_z_stride, es, pl.Lc, "out_z")))))
+    return r;
   if (pl.total_fwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_fwd))
     return fail(S6_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", pl.total_fwd,
                 a->workspace ? a->workspace_bytes : (size_t)0);
@@ -287,7 +304,7 @@ int s6_fwd(const S6FwdArgs* a, void* stream) {
     e = s6::launch_fill(a->last_state, (int64_t)p.nseq * p.dim * p.dstate, 0.f, st);
   if (e == hipSuccess) {
     s6::FwdK k = fill_fwd(*a, pl);
-    e = s6::launch_fwd(k, p.io_dtype, p.bc_dtype, st);
+    e = s6::launch_fwd(k, p.io_dtype, p.bc_dtype, st, a->kernel_events);
   }
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_fwd: %s", hipGetErrorString(e));
   return ok();
@@ -365,7 +382,7 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.K = pl.K; k.Lc = pl.Lc;
     k.nDblk = pl.nDblk64; k.nJ4 = pl.nJ256;
     k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
-    e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st);
+    e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st, a->kernel_events);
   }
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_bwd: %s", hipGetErrorString(e));
   return ok();

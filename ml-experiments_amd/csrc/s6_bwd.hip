@@ -372,8 +372,13 @@ __global__ void __launch_bounds__(256) bwd_reduce_bc(BwdK p) {
   }
 }
 
+static hipError_t record(void* const* ev, int i, hipStream_t st) {
+  if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
+  return hipEventRecord((hipEvent_t)ev[i], st);
+}
+
 template <typename Tio, typename Tbc, bool VARLEN>
-static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st) {
+static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st, void* const* ev) {
   hipError_t e;
   if (k.K > 1) {
     dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)(k.K - 1));
@@ -384,8 +389,10 @@ static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   dim3 grid((unsigned)(k.Bsz * k.G * k.nJ4), (unsigned)k.K);
+  if ((e = record(ev, 0, st)) != hipSuccess) return e;
   hipLaunchKernelGGL((bwd_main<Tio, Tbc, VARLEN>), grid, dim3(256), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = record(ev, 1, st)) != hipSuccess) return e;
   const int64_t total = k.Bsz * k.G * k.L * k.N;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65535) blocks = 65535;
@@ -394,24 +401,25 @@ static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st) {
 }
 
 template <typename Tio, typename Tbc>
-static hipError_t launch_bwd_v(const BwdK& k, hipStream_t st) {
-  return k.nseq > 0 ? launch_bwd_t<Tio, Tbc, true>(k, st) : launch_bwd_t<Tio, Tbc, false>(k, st);
+static hipError_t launch_bwd_v(const BwdK& k, hipStream_t st, void* const* ev) {
+  return k.nseq > 0 ? launch_bwd_t<Tio, Tbc, true>(k, st, ev)
+                    : launch_bwd_t<Tio, Tbc, false>(k, st, ev);
 }
 
 template <typename Tio>
-static hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st) {
+static hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
   switch (bc_dtype) {
-    case S6_F32: return launch_bwd_v<Tio, float>(k, st);
-    case S6_BF16: return launch_bwd_v<Tio, bf16>(k, st);
-    default: return launch_bwd_v<Tio, f16>(k, st);
+    case S6_F32: return launch_bwd_v<Tio, float>(k, st, ev);
+    case S6_BF16: return launch_bwd_v<Tio, bf16>(k, st, ev);
+    default: return launch_bwd_v<Tio, f16>(k, st, ev);
   }
 }
 
-hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st) {
+hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev) {
   switch (io_dtype) {
-    case S6_F32: return launch_bwd_io<float>(k, bc_dtype, st);
-    case S6_BF16: return launch_bwd_io<bf16>(k, bc_dtype, st);
-    default: return launch_bwd_io<f16>(k, bc_dtype, st);
+    case S6_F32: return launch_bwd_io<float>(k, bc_dtype, st, ev);
+    case S6_BF16: return launch_bwd_io<bf16>(k, bc_dtype, st, ev);
+    default: return launch_bwd_io<f16>(k, bc_dtype, st, ev);
   }
 }
 

@@ -47,42 +47,108 @@ template <> struct Elem<f16> {
   }
 };
 
+// Raw buffer access.  Each wave addresses its tensors through a buffer resource whose base
+// is the wave's first element; a lane's channel offset goes in the VGPR offset and the time
+// offset, identical for all lanes, in the SGPR offset, so stepping in time costs no VALU
+// address arithmetic.  Lanes past the last channel get kOffDrop: their loads return 0 and
+// their stores are dropped by the buffer range check (num_records = kBufRecords).
+constexpr uint32_t kBufRecords = 0x7fffffffu;
+constexpr uint32_t kOffDrop = 0x80000000u;
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)kBufRecords,
+                                           0x00020000);
+}
+
+template <typename T> struct Buf;
+template <> struct Buf<float> {
+  __device__ static inline float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0));
+  }
+  __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)vo, (int)so, 0);
+  }
+};
+template <> struct Buf<bf16> {
+  __device__ static inline float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
+    return __uint_as_float(b << 16);
+  }
+  __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+    const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+    __builtin_amdgcn_raw_buffer_store_b16(b, r, (int)vo, (int)so, 0);
+  }
+};
+template <> struct Buf<f16> {
+  __device__ static inline float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    const uint16_t b = __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
+    return (float)__builtin_bit_cast(_Float16, b);
+  }
+  __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+    const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    __builtin_amdgcn_raw_buffer_store_b16(b, r, (int)vo, (int)so, 0);
+  }
+};
+
 // Uniform (wave-invariant) loads of B_t / C_t through the scalar cache.  The pointer is
 // cast to the constant address space so a uniform address is selected as s_load; the
 // 16-bit formats are loaded as packed 32-bit pairs and unpacked on the scalar unit.
 typedef const __attribute__((address_space(4))) uint32_t* cu32p;
 
-template <typename T> struct BCLoad;
-template <> struct BCLoad<float> {
-  // row points at element n=0 of a time step; the row holds NS valid (or zero-padded) values.
-  template <int NS>
-  __device__ static inline void row(const void* row, float (&v)[NS]) {
+// A group of up to 16 consecutive states of one B or C row, as raw 32-bit words in SGPRs.
+// The 16-bit formats stay packed two per word until the value is used.
+template <typename T> struct BCGroup;
+template <> struct BCGroup<float> {
+  static constexpr int kWords = 16;
+  uint32_t w[16];
+  template <int G>
+  __device__ inline void load(const char* row) {
     cu32p r = (cu32p)row;
 #pragma unroll
-    for (int n = 0; n < NS; ++n) v[n] = __uint_as_float(r[n]);
+    for (int i = 0; i < G; ++i) w[i] = r[i];
+  }
+  __device__ inline float get(int n) const { return __uint_as_float(w[n]); }
+};
+template <> struct BCGroup<bf16> {
+  static constexpr int kWords = 8;
+  uint32_t w[8];
+  template <int G>
+  __device__ inline void load(const char* row) {
+    cu32p r = (cu32p)row;
+#pragma unroll
+    for (int i = 0; i < G / 2; ++i) w[i] = r[i];
+  }
+  __device__ inline float get(int n) const {
+    const uint32_t x = w[n >> 1];
+    return (n & 1) ? __uint_as_float(x & 0xffff0000u) : __uint_as_float(x << 16);
   }
 };
-template <> struct BCLoad<bf16> {
-  template <int NS>
-  __device__ static inline void row(const void* row, float (&v)[NS]) {
+template <> struct BCGroup<f16> {
+  static constexpr int kWords = 8;
+  uint32_t w[8];
+  template <int G>
+  __device__ inline void load(const char* row) {
     cu32p r = (cu32p)row;
 #pragma unroll
-    for (int n = 0; n < NS; n += 2) {
-      const uint32_t w = r[n / 2];
-      v[n] = __uint_as_float(w << 16);
-      v[n + 1] = __uint_as_float(w & 0xffff0000u);
-    }
+    for (int i = 0; i < G / 2; ++i) w[i] = r[i];
+  }
+  __device__ inline float get(int n) const {
+    const uint32_t x = w[n >> 1];
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((n & 1) ? (x >> 16) : (x & 0xffffu)));
   }
 };
-template <> struct BCLoad<f16> {
+
+// Whole-row loads (NS values) for the backward kernels.
+template <typename T> struct BCLoad {
   template <int NS>
   __device__ static inline void row(const void* row, float (&v)[NS]) {
-    cu32p r = (cu32p)row;
+    static_assert(NS % 16 == 0 || NS < 16, "row width");
+    constexpr int G = NS < 16 ? NS : 16;
 #pragma unroll
-    for (int n = 0; n < NS; n += 2) {
-      const uint32_t w = r[n / 2];
-      v[n] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
-      v[n + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    for (int g0 = 0; g0 < NS; g0 += G) {
+      BCGroup<T> grp;
+      grp.template load<G>((const char*)row + g0 * Elem<T>::kSize);
+#pragma unroll
+      for (int n = 0; n < G; ++n) v[g0 + n] = grp.get(n);
     }
   }
 };

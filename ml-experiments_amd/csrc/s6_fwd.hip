@@ -39,6 +39,8 @@ __device__ inline SeqCursor seq_cursor_at(const int32_t* cu, int32_t nseq, int64
 
 template <typename Tio, typename Tbc, int NS, bool FULL, bool VARLEN>
 __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
+  constexpr int TB = 8;  // time steps per unrolled block; divides kCk
+  constexpr int ES = Elem<Tio>::kSize;
   const int lane = threadIdx.x;
   const int64_t Dg = p.D / p.G;
   const int64_t nJ = (Dg + kWave - 1) / kWave;
@@ -49,12 +51,12 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const int64_t j = rem % nJ;
   const int64_t dloc = j * kWave + lane;
   const bool active = dloc < Dg;
+  const int64_t d0 = g * Dg + j * kWave;  // first channel of this wave
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
   const int64_t c = blockIdx.y;
   const int64_t t0 = c * p.Lc;
   const int64_t t1 = min(t0 + p.Lc, p.L);
   const int N = (int)p.N;
-  constexpr int ES = Elem<Tio>::kSize;
 
   float Ap[NS];
   float h[NS];
@@ -71,90 +73,141 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   }
   const float bias = p.has_bias ? p.bias[d * p.sbias] : 0.f;
   const float Dv = (FULL && p.has_D) ? p.Dp[d * p.sD] : 0.f;
+  const bool has_z = FULL && p.has_z;
+  const bool softplus = p.softplus != 0;
 
-  // Per-lane byte pointers, advanced by one time step per iteration.
-  const char* up = (const char*)p.u + (b * p.su[0] + d * p.su[1] + t0 * p.su[2]) * ES;
-  const char* dp = (const char*)p.delta + (b * p.sdl[0] + d * p.sdl[1] + t0 * p.sdl[2]) * ES;
-  const char* zp = FULL && p.has_z ? (const char*)p.z + (b * p.sz[0] + d * p.sz[1] + t0 * p.sz[2]) * ES : nullptr;
-  char* op = FULL ? (char*)p.out + (b * p.so[0] + d * p.so[1] + t0 * p.so[2]) * ES : nullptr;
-  char* ozp = FULL && p.has_z ? (char*)p.out_z + (b * p.soz[0] + d * p.soz[1] + t0 * p.soz[2]) * ES : nullptr;
-  const int64_t ust = p.su[2] * ES, dst = p.sdl[2] * ES, zst = p.sz[2] * ES, ost = p.so[2] * ES,
-                ozst = p.soz[2] * ES;
+  // Buffer resources based at (b, d0, t0) of each [batch, dim, seqlen] tensor.
+  const auto rs_u = make_rsrc((const char*)p.u + (b * p.su[0] + d0 * p.su[1] + t0 * p.su[2]) * ES);
+  const auto rs_d = make_rsrc((const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1] + t0 * p.sdl[2]) * ES);
+  const uint32_t vo_u = active ? (uint32_t)(lane * p.su[1] * ES) : kOffDrop;
+  const uint32_t vo_d = active ? (uint32_t)(lane * p.sdl[1] * ES) : kOffDrop;
+  const uint32_t st_u = (uint32_t)(p.su[2] * ES), st_d = (uint32_t)(p.sdl[2] * ES);
+  // Unused resources (no output in the summary pass, no z) point at u and are never read.
+  const auto rs_o = make_rsrc(FULL ? (const char*)p.out + (b * p.so[0] + d0 * p.so[1] + t0 * p.so[2]) * ES
+                                   : (const char*)p.u);
+  const auto rs_z = make_rsrc(has_z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1] + t0 * p.sz[2]) * ES
+                                    : (const char*)p.u);
+  const auto rs_oz = make_rsrc(has_z ? (const char*)p.out_z + (b * p.soz[0] + d0 * p.soz[1] + t0 * p.soz[2]) * ES
+                                     : (const char*)p.u);
+  const uint32_t vo_o = (FULL && active) ? (uint32_t)(lane * p.so[1] * ES) : kOffDrop;
+  const uint32_t vo_z = (has_z && active) ? (uint32_t)(lane * p.sz[1] * ES) : kOffDrop;
+  const uint32_t vo_oz = (has_z && active) ? (uint32_t)(lane * p.soz[1] * ES) : kOffDrop;
+  const uint32_t st_o = FULL ? (uint32_t)(p.so[2] * ES) : 0u;
+  const uint32_t st_z = has_z ? (uint32_t)(p.sz[2] * ES) : 0u;
+  const uint32_t st_oz = has_z ? (uint32_t)(p.soz[2] * ES) : 0u;
   const char* Brow = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + t0 * p.sB[3]) * Elem<Tbc>::kSize;
   const char* Crow = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + t0 * p.sC[3]) * Elem<Tbc>::kSize;
   const int64_t Bstep = p.sB[3] * Elem<Tbc>::kSize;
   const int64_t Cstep = p.sC[3] * Elem<Tbc>::kSize;
-  const bool has_z = FULL && p.has_z;
-  const bool softplus = p.softplus != 0;
 
   SeqCursor sc;
   if (VARLEN) sc = seq_cursor_at(p.cu, p.nseq, t0);
   float ssum = 0.f;  // sum of Delta since the last sequence start (chunk summary only)
 
-  // Blocks of kCk steps end exactly on checkpoint boundaries (t0 is a multiple of kCk).
-  for (int64_t tb = t0; tb < t1; tb += kCk) {
-    const int64_t te = min(tb + (int64_t)kCk, t1);
-    for (int64_t t = tb; t < te; ++t) {
-      if (VARLEN && t == sc.pending) {
+  // Register double buffer: the next block's u / delta / z are in flight while the
+  // current block computes.  Loads past t1 re-read step t1 - 1.
+  float un[TB], dn[TB], zn[TB];
+  auto fetch = [&](int64_t tb) {
 #pragma unroll
-        for (int n = 0; n < NS; ++n) h[n] = 0.f;
-        ssum = 0.f;
-        while (sc.idx <= p.nseq && (int64_t)p.cu[sc.idx] <= t) ++sc.idx;
-        sc.pending = (sc.idx <= p.nseq) ? (int64_t)p.cu[sc.idx] : INT64_MAX;
-      }
-      float Bv[NS];
-      BCLoad<Tbc>::template row<NS>(Brow, Bv);
-      Brow += Bstep;
-      float Cv[NS];
-      if (FULL) {
-        BCLoad<Tbc>::template row<NS>(Crow, Cv);
-        Crow += Cstep;
-      }
-      const float uu = Elem<Tio>::load(up, 0);
-      float dt = Elem<Tio>::load(dp, 0) + bias;
-      up += ust;
-      dp += dst;
-      if (softplus) dt = softplus20(dt);
-      const float dtu = dt * uu;
-      float y = 0.f;
-#pragma unroll
-      for (int n = 0; n < NS; ++n) {
-        const float a = fast_exp2(dt * Ap[n]);
-        h[n] = fmaf(a, h[n], dtu * Bv[n]);
-        if (FULL) y = fmaf(Cv[n], h[n], y);
-      }
-      if (!FULL) {
-        ssum += dt;
-      } else {
-        y = fmaf(uu, Dv, y);
-        if (active) Elem<Tio>::store(op, 0, y);
-        op += ost;
-        if (has_z) {
-          const float zz = Elem<Tio>::load(zp, 0);
-          if (active) Elem<Tio>::store(ozp, 0, y * zz * sigmoidf_(zz));
-          zp += zst;
-          ozp += ozst;
-        }
-        if (VARLEN && p.last_state != nullptr && active && (t + 1 == sc.pending || t == p.L - 1)) {
-          float* ls = p.last_state + ((int64_t)(sc.idx - 1) * p.D + d) * p.N;
-#pragma unroll
-          for (int n = 0; n < NS; ++n)
-            if (n < N) ls[n] = h[n];
-        }
-      }
+    for (int i = 0; i < TB; ++i) {
+      const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
+      un[i] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
+      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
+      if (has_z) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
     }
-    if (FULL && active) {
-      if (p.x_ckpt != nullptr) {
-        float* xc = p.x_ckpt + (ch * p.nck + (te - 1) / kCk) * p.N;
+  };
+  fetch(t0);
+
+  // B_t / C_t arrive through the scalar cache one group of G states ahead of their use;
+  // the scheduling barrier after each group keeps the compiler from hoisting every row of
+  // the unrolled block into SGPRs at once.
+  constexpr int G = NS < 16 ? NS : 16;
+  constexpr int NG = NS / G;
+  constexpr int EB = Elem<Tbc>::kSize;
+  BCGroup<Tbc> bnx, cnx;
+  bnx.template load<G>(Brow);
+  if (FULL) cnx.template load<G>(Crow);
+
+  for (int64_t tb = t0; tb < t1; tb += TB) {
+    float uc[TB], dc[TB], zc[TB];
 #pragma unroll
-        for (int n = 0; n < NS; ++n)
-          if (n < N) xc[n] = h[n];
-      }
-      if (!VARLEN && p.last_state != nullptr && te == p.L) {
-        float* ls = p.last_state + ch * p.N;
+    for (int i = 0; i < TB; ++i) {
+      uc[i] = un[i];
+      dc[i] = dn[i];
+      zc[i] = has_z ? zn[i] : 0.f;
+    }
+    if (tb + TB < t1) fetch(tb + TB);
 #pragma unroll
-        for (int n = 0; n < NS; ++n)
-          if (n < N) ls[n] = h[n];
+    for (int i = 0; i < TB; ++i) {
+      const int64_t t = tb + i;
+      if (t < t1) {
+        if (VARLEN && t == sc.pending) {
+#pragma unroll
+          for (int n = 0; n < NS; ++n) h[n] = 0.f;
+          ssum = 0.f;
+          while (sc.idx <= p.nseq && (int64_t)p.cu[sc.idx] <= t) ++sc.idx;
+          sc.pending = (sc.idx <= p.nseq) ? (int64_t)p.cu[sc.idx] : INT64_MAX;
+        }
+        const uint32_t r = (uint32_t)(t - t0);
+        const uint32_t rn = (uint32_t)(min(t + 1, t1 - 1) - t0);
+        const float uu = uc[i];
+        float dt = dc[i] + bias;
+        if (softplus) dt = softplus20(dt);
+        const float dtu = dt * uu;
+        // y accumulates in 4 independent FMA chains (n mod 4): shorter dependency chains
+        // and a smaller rounding error than one long chain.
+        float ys[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          const BCGroup<Tbc> bcur = bnx;
+          BCGroup<Tbc> ccur;
+          if (FULL) ccur = cnx;
+          const int64_t off_b = (gi + 1 < NG) ? ((int64_t)r * Bstep + (gi + 1) * G * EB) : (int64_t)rn * Bstep;
+          bnx.template load<G>(Brow + off_b);
+          if (FULL) {
+            const int64_t off_c = (gi + 1 < NG) ? ((int64_t)r * Cstep + (gi + 1) * G * EB) : (int64_t)rn * Cstep;
+            cnx.template load<G>(Crow + off_c);
+          }
+#pragma unroll
+          for (int k = 0; k < G; ++k) {
+            const int n = gi * G + k;
+            const float a = fast_exp2(dt * Ap[n]);
+            h[n] = fmaf(a, h[n], dtu * bcur.get(k));
+            if (FULL) ys[k & 3] = fmaf(ccur.get(k), h[n], ys[k & 3]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!FULL) {
+          ssum += dt;
+        } else {
+          float y = (ys[0] + ys[1]) + (ys[2] + ys[3]);
+          y = fmaf(uu, Dv, y);
+          Buf<Tio>::store(rs_o, vo_o, r * st_o, y);
+          if (has_z) {
+            const float zz = zc[i];
+            Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
+          }
+          if (VARLEN && p.last_state != nullptr && active && (t + 1 == sc.pending || t == p.L - 1)) {
+            float* ls = p.last_state + ((int64_t)(sc.idx - 1) * p.D + d) * p.N;
+#pragma unroll
+            for (int n = 0; n < NS; ++n)
+              if (n < N) ls[n] = h[n];
+          }
+          if (((t + 1) % kCk == 0 || t == p.L - 1) && active) {
+            if (p.x_ckpt != nullptr) {
+              float* xc = p.x_ckpt + (ch * p.nck + t / kCk) * p.N;
+#pragma unroll
+              for (int n = 0; n < NS; ++n)
+                if (n < N) xc[n] = h[n];
+            }
+            if (!VARLEN && p.last_state != nullptr && t == p.L - 1) {
+              float* ls = p.last_state + ch * p.N;
+#pragma unroll
+              for (int n = 0; n < NS; ++n)
+                if (n < N) ls[n] = h[n];
+            }
+          }
+        }
       }
     }
   }
@@ -224,12 +277,18 @@ __global__ void relayout_bc(const T* __restrict__ src, int64_t s0, int64_t s1, i
 // Host-side launch helpers
 // ---------------------------------------------------------------------------------------
 
+static hipError_t record(void* const* ev, int i, hipStream_t st) {
+  if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
+  return hipEventRecord((hipEvent_t)ev[i], st);
+}
+
 template <typename Tio, typename Tbc, int NS, bool VARLEN>
-static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st) {
+static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st, void* const* ev) {
+  hipError_t e = hipSuccess;
   if (k.K > 1) {
     dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)(k.K - 1));
     hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, false, VARLEN>), grid, dim3(kWave), 0, st, k);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t total = k.Bsz * k.D * k.N;
     hipLaunchKernelGGL(fwd_carry, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, k);
@@ -237,38 +296,42 @@ static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)k.K);
+  e = record(ev, 0, st);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, true, VARLEN>), grid, dim3(kWave), 0, st, k);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return record(ev, 1, st);
 }
 
 template <typename Tio, typename Tbc, int NS>
-static hipError_t launch_ns(const FwdK& k, hipStream_t st) {
-  return k.nseq > 0 ? launch_scan_pair<Tio, Tbc, NS, true>(k, st)
-                    : launch_scan_pair<Tio, Tbc, NS, false>(k, st);
+static hipError_t launch_ns(const FwdK& k, hipStream_t st, void* const* ev) {
+  return k.nseq > 0 ? launch_scan_pair<Tio, Tbc, NS, true>(k, st, ev)
+                    : launch_scan_pair<Tio, Tbc, NS, false>(k, st, ev);
 }
 
 template <typename Tio, typename Tbc>
-static hipError_t launch_bc(const FwdK& k, hipStream_t st) {
-  if (k.N <= 8) return launch_ns<Tio, Tbc, 8>(k, st);
-  if (k.N <= 16) return launch_ns<Tio, Tbc, 16>(k, st);
-  if (k.N <= 32) return launch_ns<Tio, Tbc, 32>(k, st);
-  return launch_ns<Tio, Tbc, 64>(k, st);
+static hipError_t launch_bc(const FwdK& k, hipStream_t st, void* const* ev) {
+  if (k.N <= 8) return launch_ns<Tio, Tbc, 8>(k, st, ev);
+  if (k.N <= 16) return launch_ns<Tio, Tbc, 16>(k, st, ev);
+  if (k.N <= 32) return launch_ns<Tio, Tbc, 32>(k, st, ev);
+  return launch_ns<Tio, Tbc, 64>(k, st, ev);
 }
 
 template <typename Tio>
-static hipError_t launch_io(const FwdK& k, int bc_dtype, hipStream_t st) {
+static hipError_t launch_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
   switch (bc_dtype) {
-    case S6_F32: return launch_bc<Tio, float>(k, st);
-    case S6_BF16: return launch_bc<Tio, bf16>(k, st);
-    default: return launch_bc<Tio, f16>(k, st);
+    case S6_F32: return launch_bc<Tio, float>(k, st, ev);
+    case S6_BF16: return launch_bc<Tio, bf16>(k, st, ev);
+    default: return launch_bc<Tio, f16>(k, st, ev);
   }
 }
 
-hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st) {
+hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev) {
   switch (io_dtype) {
-    case S6_F32: return launch_io<float>(k, bc_dtype, st);
-    case S6_BF16: return launch_io<bf16>(k, bc_dtype, st);
-    default: return launch_io<f16>(k, bc_dtype, st);
+    case S6_F32: return launch_io<float>(k, bc_dtype, st, ev);
+    case S6_BF16: return launch_io<bf16>(k, bc_dtype, st, ev);
+    default: return launch_io<f16>(k, bc_dtype, st, ev);
   }
 }
 

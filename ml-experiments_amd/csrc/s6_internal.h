@@ -29,8 +29,9 @@ struct BwdK {
   int32_t has_D, has_z, has_bias, softplus;
 };
 
-hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st);
-hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st);
+// ev (nullable): hipEvent_t pair recorded around the main scan kernel.
+hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev);
+hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev);
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
 hipError_t launch_relayout(const void* src, const int64_t s[4], int esize, void* dst,
                            int64_t Bsz, int64_t G, int64_t N, int64_t NP, int64_t L,

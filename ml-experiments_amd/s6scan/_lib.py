@@ -59,6 +59,7 @@ class S6FwdArgs(ctypes.Structure):
         ("x_ckpt", _vp),
         ("last_state", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("kernel_events", _vp * 2),
     ]
 
 
@@ -86,6 +87,7 @@ class S6BwdArgs(ctypes.Structure):
         ("dz", _vp), ("dz_stride", _a(3)),
         ("ddelta_bias", _vp), ("ddelta_bias_stride", _i64),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("kernel_events", _vp * 2),
     ]
 
 

@@ -121,11 +121,20 @@ def _as4(M):
     return M.unsqueeze(1) if M.dim() == 3 else M
 
 
+def _events(kernel_events):
+    """Raw hipEvent_t handles of a (torch.cuda.Event, torch.cuda.Event) pair, or NULLs."""
+    if kernel_events is None:
+        return (None, None)
+    return tuple(ctypes.c_void_p(e.cuda_event) for e in kernel_events)
+
+
 def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
                            delta_softplus=False, cu_seqlens=None, want_ckpt=True,
-                           want_last_state=False):
+                           want_last_state=False, kernel_events=None):
     """One forward launch.  Returns (out, out_z, x_ckpt, last_state); out_z is None without
-    z, x_ckpt is None unless ``want_ckpt``, last_state is None unless ``want_last_state``."""
+    z, x_ckpt is None unless ``want_ckpt``, last_state is None unless ``want_last_state``.
+    ``kernel_events``: optional pair of already-recorded torch.cuda.Events that the library
+    re-records around its main scan kernel (measurement only)."""
     dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
     batch, dim, seqlen, dstate, G, nseq = dims
     prob = _problem(u, B, z, D, delta_bias, delta_softplus, dims)
@@ -158,13 +167,14 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         nbytes = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=u.device)
         args.workspace, args.workspace_bytes = _ptr(ws), nbytes
+        args.kernel_events = _events(kernel_events)
         stream = torch.cuda.current_stream(u.device).cuda_stream
         _lib.check(_lib.LIB.s6_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "s6_fwd")
     return out, out_z, x_ckpt, last_state
 
 
 def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, x_ckpt,
-                            out=None, cu_seqlens=None):
+                            out=None, cu_seqlens=None, kernel_events=None):
     """One backward launch.  Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias) with dB, dC
     in B/C's own rank (3-D or 4-D) and fp32 like the reference kernel's; None for absent
     inputs."""
@@ -216,6 +226,7 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
         nbytes = _lib.LIB.s6_bwd_workspace_bytes(ctypes.byref(prob))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=u.device)
         args.workspace, args.workspace_bytes = _ptr(ws), nbytes
+        args.kernel_events = _events(kernel_events)
         stream = torch.cuda.current_stream(u.device).cuda_stream
         _lib.check(_lib.LIB.s6_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "s6_bwd")
     dB = dB4.squeeze(1) if B.dim() == 3 else dB4

@@ -89,7 +89,8 @@ def scan_fwd64(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplu
         last = h[:, :, -1]
     else:
         cu = np.asarray(cu_seqlens)
-        last = np.stack([h[0, :, int(e) - 1] for e in cu[1:]], axis=0)
+        last = np.stack([h[0, :, int(e) - 1] if int(e) > int(s) else np.zeros((dim, N))
+                         for s, e in zip(cu[:-1], cu[1:])], axis=0)
     return dict(out=out, y=y, h=h, last_state=last, Delta=Delta, abar=abar, pre=pre)
 
 

@@ -44,6 +44,8 @@ void s6o_fwd(int64_t Bsz, int64_t D, int64_t L, int64_t N, int64_t G, const floa
   unsigned char* st = (unsigned char*)malloc((size_t)L);
   starts_mask(L, cu, nseq > 0 ? nseq : 0, st);
   const int64_t Dg = D / G;
+  if (last_state && nseq > 0)  /* empty sequences keep a zero final state */
+    memset(last_state, 0, (size_t)(nseq * D * N) * sizeof(float));
 #pragma omp parallel for schedule(dynamic, 1)
   for (int64_t ch = 0; ch < Bsz * D; ++ch) {
     const int64_t b = ch / D, d = ch % D, g = d / Dg;

@@ -108,11 +108,14 @@ def selective_scan_ref_varlen(u, delta, A, B, C, cu_seqlens, D=None, z=None, del
                               compute_dtype=torch.float32):
     """Packed variable-length scan: batch 1, sequences [cu[i], cu[i+1]) scanned
     independently from a zero state.  Returns out [1, D, T] and, if asked, the
-    per-sequence final states [nseq, D, N] (fp32)."""
+    per-sequence final states [nseq, D, N] (fp32; zero for an empty sequence)."""
     assert u.shape[0] == 1
     cu = [int(v) for v in cu_seqlens.tolist()]
     outs, states = [], []
     for s, e in zip(cu[:-1], cu[1:]):
+        if e == s:  # an empty sequence produces no output and a zero final state
+            states.append(A.new_zeros((1, A.shape[0], A.shape[1]), dtype=compute_dtype))
+            continue
         sl = slice(s, e)
         sub = lambda t: None if t is None else t[..., sl]
         res = selective_scan_ref(u[..., sl], delta[..., sl], A, B[..., sl], C[..., sl], D=D,

@@ -1,0 +1,132 @@
+"""The C ABI library (libs6scan.so) without a GPU: it loads, exports every entry point that
+include/s6scan.h declares, and its host-only validation rejects bad arguments with the
+documented error codes.  No compute call is made here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from s6scan import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "s6scan.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(s6_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    declared = header_functions()
+    assert "s6_fwd" in declared and "s6_bwd" in declared
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [f for f in declared if not hasattr(lib, f)]
+    assert not missing, f"declared in s6scan.h but not exported: {missing}"
+    assert set(declared) == set(_lib.EXPORTS), "ctypes binding and header disagree"
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (S6_[A-Z_]+) (\d+)", text))
+    assert int(consts["S6_ABI_VERSION"]) == _lib.ABI_VERSION == _lib.LIB.s6_abi_version()
+    assert int(consts["S6_CKPT_INTERVAL"]) == _lib.CKPT_INTERVAL
+    assert int(consts["S6_MAX_DSTATE_FWD"]) == _lib.MAX_DSTATE_FWD
+    assert int(consts["S6_MAX_DSTATE_BWD"]) == _lib.MAX_DSTATE_BWD
+
+
+def prob(**kw):
+    base = dict(batch=2, dim=128, seqlen=100, dstate=16, ngroups=1, io_dtype=_lib.BF16,
+                bc_dtype=_lib.BF16, has_D=1, has_z=0, has_delta_bias=0, delta_softplus=0, nseq=0)
+    base.update(kw)
+    return _lib.S6Problem(**base)
+
+
+def validate(**kw):
+    return _lib.LIB.s6_validate_problem(ctypes.byref(prob(**kw)))
+
+
+def test_valid_problem():
+    assert validate() == _lib.OK
+    assert _lib.last_error() == ""
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(batch=0), _lib.E_INVALID, "must be >= 1"),
+    (dict(seqlen=0), _lib.E_INVALID, "must be >= 1"),
+    (dict(dim=100, ngroups=3), _lib.E_INVALID, "divisible"),
+    (dict(io_dtype=7), _lib.E_INVALID, "dtype"),
+    (dict(dstate=65), _lib.E_UNSUPPORTED, "dstate"),
+    (dict(nseq=-1), _lib.E_INVALID, "nseq"),
+    (dict(nseq=4, batch=2), _lib.E_INVALID, "batch == 1"),
+])
+def test_invalid_problems(kw, code, msg):
+    assert validate(**kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_num_checkpoints():
+    for L, want in ((1, 1), (32, 1), (33, 2), (4096, 128)):
+        assert _lib.LIB.s6_num_checkpoints(ctypes.byref(prob(seqlen=L))) == want
+
+
+def test_workspace_sizes_are_reported_and_grow_with_the_problem():
+    small = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob(seqlen=4096)))
+    big = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob(seqlen=4096, batch=8)))
+    assert 0 < small <= big
+    assert (_lib.LIB.s6_bwd_workspace_bytes(ctypes.byref(prob(seqlen=4096)))
+            >= _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob(seqlen=4096))))
+    assert _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob(batch=0))) == 0
+
+
+def fwd_args(**kw):
+    a = _lib.S6FwdArgs()
+    a.p = prob(**kw)
+    fake = 0x10000  # never dereferenced: validation is host-only
+    for f in ("u", "delta", "A", "B", "C", "D", "out"):
+        setattr(a, f, fake)
+    a.u_stride = a.delta_stride = a.out_stride = (a.p.dim * a.p.seqlen, a.p.seqlen, 1)
+    a.A_stride = (a.p.dstate, 1)
+    a.B_stride = a.C_stride = (a.p.dstate * a.p.seqlen, a.p.dstate * a.p.seqlen, a.p.seqlen, 1)
+    a.D_stride = 1
+    nb = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(a.p))
+    a.workspace, a.workspace_bytes = fake, nb
+    return a
+
+
+def test_validate_fwd_ok_and_errors():
+    a = fwd_args()
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.OK
+    a.u = None
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "u must not be NULL" in _lib.last_error()
+    a = fwd_args()
+    a.workspace_bytes = 8
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_WORKSPACE
+    a = fwd_args()
+    a.delta_stride = (1, -1, 1)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "negative stride" in _lib.last_error()
+    a = fwd_args(has_z=1)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "z must not be NULL" in _lib.last_error()
+    a = fwd_args(nseq=3, batch=1)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "cu_seqlens" in _lib.last_error()
+
+
+def test_validate_bwd_rejects_large_dstate():
+    a = _lib.S6BwdArgs()
+    a.p = prob(dstate=32)
+    for f in ("u", "delta", "A", "B", "C", "D", "dout", "x_ckpt", "du", "ddelta", "dA", "dB",
+              "dC", "dD"):
+        setattr(a, f, 0x10000)
+    assert _lib.LIB.s6_validate_bwd(ctypes.byref(a)) == _lib.E_UNSUPPORTED
+    assert "dstate <= 16" in _lib.last_error()
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(ImportError, match="native library not found"):
+        _lib.load_library(str(tmp_path / "libs6scan.so"))

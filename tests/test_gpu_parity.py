@@ -1,0 +1,312 @@
+"""GPU parity of the HIP S6 scan (through the C ABI, via the drop-in selective_scan_fn)
+against the CPU oracle: the torch restatement of selective_scan_ref at sizes it finishes in
+seconds, the committed golden fixtures, and the C restatement at the five workload sizes.
+Tolerances are in tests/tolerances.py."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import s6scan
+from oracle import c_oracle
+from oracle.selective_scan_ref import (selective_scan_ref, selective_scan_ref_grads,
+                                       selective_scan_ref_varlen)
+from s6scan.configs import CONFIGS, make_inputs
+from tolerances import assert_close, assert_grad_close, assert_out_close, assert_state_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "s6_golden.npz")
+
+
+def gen(B, L, D, N, dtype, seed, G=1, z=False, bias=False, shift=-1.0):
+    """Channel-last producer tensors ([B, L, *]) like the workload generator."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(B, L, D, generator=g)
+    dtr = torch.randn(B, L, D, generator=g)
+    A = -torch.exp(torch.rand(D, N, generator=g) * np.log(16.0))
+    Bm = torch.randn(B, L, G, N, generator=g)
+    Cm = torch.randn(B, L, G, N, generator=g)
+    Dv = torch.randn(D, generator=g)
+    zz = torch.randn(B, L, D, generator=g).to(dtype) if z else None
+    bb = 0.3 * torch.randn(D, generator=g) if bias else None
+    dl = (0.5 * dtr + shift) if bias else torch.nn.functional.softplus(0.5 * dtr + shift)
+    dy = torch.randn(B, L, D, generator=g).to(dtype)
+    return dict(x=x.to(dtype), delta=dl.to(dtype), A=A, B=Bm.to(dtype), C=Cm.to(dtype), D=Dv,
+                z=zz, bias=bb, dy=dy, G=G)
+
+
+def views(t, layout):
+    """[B, L, D] producer tensor -> [B, D, L] argument in the requested memory layout."""
+    if t is None:
+        return None
+    v = t.transpose(1, 2)
+    return v.contiguous() if layout == "contiguous" else v
+
+
+def bc_views(t, G, layout):
+    """[B, L, G, N] -> [B, N, L] (G == 1) or [B, G, N, L] in the requested layout."""
+    v = t.permute(0, 2, 3, 1)  # [B, G, N, L]
+    if layout in ("contiguous", "bc_lcontig"):
+        v = v.contiguous()
+    return v[:, 0] if G == 1 else v
+
+
+def call(inp, layout, device, cu=None, last=True):
+    dev = lambda t: None if t is None else t.to(device)
+    args = [views(dev(inp["x"]), layout), views(dev(inp["delta"]), layout), dev(inp["A"]),
+            bc_views(dev(inp["B"]), inp["G"], layout), bc_views(dev(inp["C"]), inp["G"], layout)]
+    kw = dict(D=dev(inp["D"]), z=views(dev(inp["z"]), layout), delta_bias=dev(inp["bias"]),
+              delta_softplus=inp["bias"] is not None, return_last_state=last)
+    return args, kw
+
+
+def ref_fwd(inp, cu=None):
+    args, kw = call(inp, "view", "cpu")
+    if cu is not None:
+        return selective_scan_ref_varlen(*args, cu, **kw)
+    return selective_scan_ref(*args, **kw)
+
+
+FWD_CASES = [
+    # B, L, D, N, dtype, G, z, bias, layout
+    (2, 300, 128, 16, torch.float32, 1, False, False, "view"),
+    (2, 300, 128, 16, torch.bfloat16, 1, False, False, "view"),
+    (2, 257, 96, 16, torch.float16, 1, True, False, "view"),
+    (1, 1, 64, 16, torch.float32, 1, False, False, "view"),
+    (3, 31, 200, 8, torch.float32, 1, True, True, "view"),
+    (2, 33, 64, 4, torch.bfloat16, 1, False, True, "view"),
+    (2, 150, 64, 12, torch.float32, 1, False, False, "view"),
+    (1, 200, 64, 24, torch.float32, 1, True, False, "view"),
+    (2, 130, 128, 32, torch.bfloat16, 1, False, False, "view"),
+    (1, 100, 64, 64, torch.float32, 1, False, True, "view"),
+    (2, 100, 256, 16, torch.float32, 2, True, True, "view"),
+    (2, 100, 192, 16, torch.bfloat16, 3, False, False, "view"),
+    (2, 129, 128, 16, torch.float32, 1, True, True, "contiguous"),
+    (2, 129, 128, 16, torch.bfloat16, 1, False, False, "contiguous"),
+    (2, 129, 128, 16, torch.bfloat16, 1, False, False, "bc_lcontig"),
+    (1, 2000, 64, 16, torch.float32, 1, False, False, "view"),
+]
+
+
+@pytest.mark.parametrize("case", FWD_CASES, ids=lambda c: "-".join(map(str, c)).replace("torch.", ""))
+def test_forward_matches_restatement(case):
+    B, L, D, N, dtype, G, z, bias, layout = case
+    inp = gen(B, L, D, N, dtype, seed=L + D + N, G=G, z=z, bias=bias)
+    out_ref, ls_ref = ref_fwd(inp)
+    args, kw = call(inp, layout, DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw)
+    assert out.dtype == dtype and out.shape == (B, D, L)
+    assert ls.dtype == torch.float32 and ls.shape == (B, D, N)
+    assert_out_close(out, out_ref, dtype, dstate=N)
+    assert_state_close(ls, ls_ref)
+
+
+def test_layouts_give_identical_results():
+    inp = gen(2, 200, 128, 16, torch.bfloat16, seed=5, z=True, bias=True)
+    res = []
+    for layout in ("view", "contiguous", "bc_lcontig"):
+        args, kw = call(inp, layout, DEV)
+        out, ls = s6scan.selective_scan_fn(*args, **kw)
+        res.append((out.contiguous(), ls))
+    for out, ls in res[1:]:
+        assert torch.equal(out, res[0][0]) and torch.equal(ls, res[0][1])
+
+
+def test_forward_is_deterministic_and_linear_in_u():
+    inp = gen(2, 500, 128, 16, torch.float32, seed=6)
+    args, kw = call(inp, "view", DEV)
+    kw.update(return_last_state=False, D=None)
+    a = s6scan.selective_scan_fn(*args, **kw)
+    b = s6scan.selective_scan_fn(*args, **kw)
+    assert torch.equal(a, b)
+    u2 = torch.randn_like(args[0])
+    c = s6scan.selective_scan_fn(3.0 * args[0] - 2.0 * u2, *args[1:], **kw)
+    d = s6scan.selective_scan_fn(u2, *args[1:], **kw)
+    # the combination 3a - 2d carries ~5x the rounding of one output
+    assert_close(c, 3.0 * a - 2.0 * d, 5e-5, 5e-6, "linearity")
+
+
+def _golden():
+    with np.load(GOLDEN) as z:
+        return {n: {k.split("/", 1)[1]: z[k] for k in z.files if k.startswith(n + "/")}
+                for n in sorted({k.split("/")[0] for k in z.files})}
+
+
+@pytest.mark.parametrize("name", sorted(_golden().keys()))
+def test_golden_fixtures(name):
+    d = _golden()[name]
+    dtype = torch.bfloat16 if name.startswith("bf16") else torch.float32
+    t = lambda k, dt=torch.float32: torch.from_numpy(d[k]).to(DEV).to(dt) if k in d else None
+    z = t("z", dtype)
+    bias = t("delta_bias")
+    cu = t("cu_seqlens", torch.int32)
+    req = "ref_du" in d
+    ins = [t("u", dtype), t("delta", dtype), t("A"), t("B", dtype), t("C", dtype), t("D")]
+    if req:
+        for x in ins + [z, bias]:
+            if x is not None:
+                x.requires_grad_()
+    out, ls = s6scan.selective_scan_fn(*ins[:5], D=ins[5], z=z, delta_bias=bias,
+                                       delta_softplus=bias is not None, return_last_state=True,
+                                       cu_seqlens=cu)
+    ref = torch.from_numpy(d["ref_out"])
+    assert_out_close(out, ref.to(dtype) if dtype != torch.float32 else ref, dtype,
+                     dstate=d["A"].shape[1])
+    assert_state_close(ls, torch.from_numpy(d["ref_last_state"]))
+    if req:
+        out.backward(torch.from_numpy(d["dout"]).to(DEV).to(dtype))
+        names = ["du", "ddelta", "dA", "dB", "dC", "dD"]
+        for nm, x in zip(names, ins):
+            assert_grad_close(x.grad, torch.from_numpy(d["ref_" + nm]), dtype, nm)
+        if z is not None:
+            assert_grad_close(z.grad, torch.from_numpy(d["ref_dz"]), dtype, "dz")
+        if bias is not None:
+            assert_grad_close(bias.grad, torch.from_numpy(d["ref_ddelta_bias"]), dtype, "dbias")
+
+
+BWD_CASES = [
+    # B, L, D, N, dtype, G, z, bias
+    (2, 200, 64, 16, torch.float32, 1, False, False),
+    (1, 333, 256, 16, torch.float32, 1, True, True),
+    (2, 256, 128, 16, torch.bfloat16, 1, True, True),
+    (2, 100, 96, 8, torch.float32, 1, False, True),
+    (1, 77, 64, 12, torch.float16, 1, True, False),
+    (2, 90, 512, 16, torch.float32, 2, False, False),
+    (1, 31, 300, 16, torch.float32, 1, False, False),
+    (1, 1, 64, 16, torch.float32, 1, True, True),
+]
+
+
+def _grads_vs_ref(inp, cu=None, layout="view"):
+    dtype = inp["x"].dtype
+    names = ["x", "delta", "A", "B", "C", "D", "z", "bias"]
+    leaves = {k: (inp[k].to(DEV).requires_grad_() if inp[k] is not None else None) for k in names}
+    g = dict(inp, **leaves)
+    args, kw = call(g, layout, DEV)
+    kw["return_last_state"] = False
+    out = s6scan.selective_scan_fn(*args, **kw, cu_seqlens=None if cu is None else cu.to(DEV))
+    out.backward(views(inp["dy"].to(DEV), layout))
+    rargs, rkw = call(inp, "view", "cpu")
+    rkw.pop("return_last_state")
+    r = selective_scan_ref_grads(*rargs, rkw["D"], views(inp["dy"], "view"), z=rkw["z"],
+                                 delta_bias=rkw["delta_bias"], delta_softplus=rkw["delta_softplus"],
+                                 cu_seqlens=cu)
+    pairs = [("x", "du", True), ("delta", "ddelta", True), ("A", "dA", False), ("B", "dB", "bc"),
+             ("C", "dC", "bc"), ("D", "dD", False), ("z", "dz", True), ("bias", "ddelta_bias", False)]
+    for leaf, rk, kind in pairs:
+        x = leaves[leaf]
+        if x is None:
+            continue
+        got = x.grad
+        if kind is True:
+            got = got.transpose(1, 2)
+        elif kind == "bc":
+            got = got.permute(0, 2, 3, 1)
+            got = got[:, 0] if inp["G"] == 1 else got
+        assert_grad_close(got, r[rk], dtype, rk)
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: "-".join(map(str, c)).replace("torch.", ""))
+def test_backward_matches_autograd_of_restatement(case):
+    B, L, D, N, dtype, G, z, bias = case
+    inp = gen(B, L, D, N, dtype, seed=100 + L, G=G, z=z, bias=bias)
+    _grads_vs_ref(inp)
+
+
+def test_backward_contiguous_layout():
+    inp = gen(2, 160, 128, 16, torch.bfloat16, seed=9, z=True, bias=True)
+    _grads_vs_ref(inp, layout="contiguous")
+
+
+@pytest.mark.parametrize("cu", [[0, 100, 101, 450, 700, 1000], [0, 32, 64, 96, 1000], [0, 1000]])
+def test_varlen_forward_and_backward(cu):
+    inp = gen(1, 1000, 64, 16, torch.float32, seed=11, z=True, bias=True)
+    cu = torch.tensor(cu, dtype=torch.int32)
+    out_ref, ls_ref = ref_fwd(inp, cu)
+    args, kw = call(inp, "view", DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw, cu_seqlens=cu.to(DEV))
+    assert ls.shape == (cu.numel() - 1, 64, 16)
+    assert_out_close(out, out_ref, torch.float32)
+    assert_state_close(ls, ls_ref)
+    _grads_vs_ref(inp, cu)
+
+
+def test_varlen_equals_independent_sequences_on_gpu():
+    inp = gen(1, 3000, 128, 16, torch.bfloat16, seed=12)
+    cu = torch.tensor([0, 700, 701, 1900, 3000], dtype=torch.int32)
+    args, kw = call(inp, "view", DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw, cu_seqlens=cu.to(DEV))
+    for i in range(4):
+        s, e = int(cu[i]), int(cu[i + 1])
+        sub = [a[..., s:e] for a in args[:2]] + [args[2]] + [a[..., s:e] for a in args[3:5]]
+        o, l = s6scan.selective_scan_fn(*sub, **kw)
+        assert torch.equal(o, out[..., s:e])
+        assert torch.equal(l[0], ls[i])
+
+
+def test_autograd_contract():
+    inp = gen(2, 64, 64, 16, torch.float32, seed=13)
+    args, kw = call(inp, "view", DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw)
+    assert not ls.requires_grad
+    x = args[0].detach().requires_grad_()
+    out, ls = s6scan.selective_scan_fn(x, *args[1:], **kw)
+    assert out.requires_grad and not ls.requires_grad
+    out.sum().backward()
+    assert x.grad is not None and x.grad.shape == x.shape
+
+
+# ------------------------------------------------------------------ workload sizes
+
+def _cfg_inputs(k, **kw):
+    return make_inputs(CONFIGS[k], **kw)
+
+
+def test_config0_full_vs_restatement():
+    cfg = CONFIGS[0]
+    i = _cfg_inputs(0)
+    ref, ref_ls = selective_scan_ref(i["x"].mT, i["delta"].mT, i["A"], i["B"].mT, i["C"].mT,
+                                     D=i["D"], return_last_state=True)
+    g = {k: v.to(DEV) for k, v in i.items()}
+    out, ls = s6scan.selective_scan_fn(g["x"].mT, g["delta"].mT, g["A"], g["B"].mT, g["C"].mT,
+                                       D=g["D"], return_last_state=True)
+    assert_out_close(out, ref, cfg.dtype, "y")
+    assert_state_close(ls, ref_ls)
+
+
+@pytest.mark.parametrize("k", [1, 2])
+def test_forward_configs_full_size_vs_c_oracle(k):
+    cfg = CONFIGS[k]
+    i = _cfg_inputs(k)
+    ref, ref_ls = c_oracle.fwd(i["x"].mT, i["delta"].mT, i["A"], i["B"].mT, i["C"].mT, D=i["D"])
+    g = {k2: v.to(DEV) for k2, v in i.items()}
+    out, ls = s6scan.selective_scan_fn(g["x"].mT, g["delta"].mT, g["A"], g["B"].mT, g["C"].mT,
+                                       D=g["D"], return_last_state=True)
+    assert_out_close(out, ref.to(cfg.dtype) if cfg.dtype != torch.float32 else ref, cfg.dtype, "y",
+                     dstate=cfg.dstate)
+    assert_state_close(ls, ref_ls)
+
+
+@pytest.mark.parametrize("k", [3, 4])
+def test_fwd_bwd_configs_full_size_vs_c_oracle(k):
+    cfg = CONFIGS[k]
+    i = _cfg_inputs(k)
+    cu = i.get("cu_seqlens")
+    ref, ref_ls = c_oracle.fwd(i["x"].mT, i["delta"].mT, i["A"], i["B"].mT, i["C"].mT, D=i["D"],
+                               cu_seqlens=cu)
+    rg = c_oracle.bwd(i["x"].mT, i["delta"].mT, i["A"], i["B"].mT, i["C"].mT, i["dy"].mT, D=i["D"],
+                      cu_seqlens=cu)
+    g = {k2: v.to(DEV) for k2, v in i.items()}
+    leaves = [g[n].requires_grad_() for n in ("x", "delta", "A", "B", "C", "D")]
+    out, ls = s6scan.selective_scan_fn(leaves[0].mT, leaves[1].mT, leaves[2], leaves[3].mT,
+                                       leaves[4].mT, D=leaves[5], return_last_state=True,
+                                       cu_seqlens=g.get("cu_seqlens"))
+    assert_out_close(out, ref.to(cfg.dtype), cfg.dtype, "y")
+    assert_state_close(ls, ref_ls)
+    out.backward(g["dy"].mT)
+    for nm, x, tr in zip(("du", "ddelta", "dA", "dB", "dC", "dD"), leaves,
+                         (True, True, False, True, True, False)):
+        got = x.grad.mT if tr else x.grad
+        assert_grad_close(got, rg[nm], cfg.dtype, nm)

@@ -1,0 +1,62 @@
+"""Parity tolerances of the S6 scan, written out once and used by every parity test.
+
+* fp32 outputs (y and the final state):  |a - b| <= 1e-6 + 1e-5 |b|  elementwise.
+  For dstate N > 16 the absolute term is scaled by N / 16.  y is an N-term fp32 dot
+  product whose rounding-error bound grows linearly in N.  At N = 64 both the HIP path
+  and the fp32 reference restatement sit up to ~2e-6 from the float64 value (measured),
+  so two correct fp32 implementations summing in different orders can differ by ~4e-6 on
+  outputs near zero: 31 of the 67M config-2 outputs do.
+* 16-bit outputs (bf16/fp16 y):           |a - b| <= 2e-2 |b| + 1e-4 rms(b)  elementwise.
+  The rms term covers outputs whose fp32 value sits at ~1e-6 of the output scale, where
+  the two rounding paths legitimately disagree by a whole 16-bit ulp.
+* gradients, 16-bit inputs:               |a - b| <= 2e-2 |b| + 2e-2 rms(b).
+* gradients, fp32 inputs:                 |a - b| <= 1e-4 |b| + 1e-4 rms(b).
+"""
+import torch
+
+
+def _viol(a, b, rtol, atol):
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    assert a.shape == b.shape, (a.shape, b.shape)
+    d = (a - b).abs()
+    lim = atol + rtol * b.abs()
+    bad = d > lim
+    return d, bad, lim
+
+
+def rms(b):
+    b = b.detach().float()
+    return b.pow(2).mean().sqrt().item() if b.numel() else 0.0
+
+
+def assert_close(a, b, rtol, atol, what=""):
+    d, bad, lim = _viol(a, b, rtol, atol)
+    if bad.any():
+        i = int(torch.argmax((d - lim).flatten()))
+        bb = b.detach().float().cpu().flatten()
+        aa = a.detach().float().cpu().flatten()
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{bad.numel()} elements out of tolerance "
+            f"(rtol={rtol}, atol={atol:.3g}); worst at {i}: got {aa[i].item():.9g} "
+            f"want {bb[i].item():.9g}; max|d|={d.max().item():.3g}; "
+            f"norm rel={(d.norm() / max(bb.norm().item(), 1e-30)).item():.3g}")
+
+
+def assert_out_close(a, b, dtype, what="out", dstate=None):
+    if dtype == torch.float32:
+        scale = max(1.0, dstate / 16.0) if dstate else 1.0
+        assert_close(a, b, 1e-5, 1e-6 * scale, what)
+    else:
+        assert_close(a, b, 2e-2, 1e-4 * rms(b), what)
+
+
+def assert_state_close(a, b, what="last_state"):
+    assert_close(a, b, 1e-5, 1e-6, what)
+
+
+def assert_grad_close(a, b, dtype, what="grad"):
+    if dtype == torch.float32:
+        assert_close(a, b, 1e-4, 1e-4 * rms(b), what)
+    else:
+        assert_close(a, b, 2e-2, 2e-2 * rms(b), what)
