@@ -37,10 +37,28 @@ __device__ inline SeqCursor seq_cursor_at(const int32_t* cu, int32_t nseq, int64
   return s;
 }
 
-template <typename Tio, typename Tbc, int NS, bool FULL, bool VARLEN>
+// Stores n < N states of one lane (NS registers) to a contiguous fp32 row.
+template <int NS>
+__device__ inline void store_state(float* dst, const float (&h)[NS], int N) {
+  if (N == NS && (NS % 4) == 0) {
+#pragma unroll
+    for (int n = 0; n < NS; n += 4)
+      *reinterpret_cast<float4*>(dst + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+  } else {
+    for (int n = 0; n < N; ++n) dst[n] = h[n];  // N < NS: dynamic count, rare
+  }
+}
+
+// MODE 0: chunk summary; 1: output pass; 2: output pass with the silu(z) gate.
+template <typename Tio, typename Tbc, int NS, int MODE, bool VARLEN>
 __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
+  constexpr bool FULL = MODE != 0;
+  constexpr bool HAS_Z = MODE == 2;
   constexpr int TB = 8;  // time steps per unrolled block; divides kCk
   constexpr int ES = Elem<Tio>::kSize;
+  constexpr int G = NS < 32 / Elem<Tbc>::kSize ? NS : 32 / Elem<Tbc>::kSize;  // 8 words per scalar-cache group
+  constexpr int NG = NS / G;
+  constexpr int EB = Elem<Tbc>::kSize;
   const int lane = threadIdx.x;
   const int64_t Dg = p.D / p.G;
   const int64_t nJ = (Dg + kWave - 1) / kWave;
@@ -53,9 +71,10 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const bool active = dloc < Dg;
   const int64_t d0 = g * Dg + j * kWave;  // first channel of this wave
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int64_t c = blockIdx.y;
-  const int64_t t0 = c * p.Lc;
-  const int64_t t1 = min(t0 + p.Lc, p.L);
+  const int c = blockIdx.y;
+  const int L = (int)p.L;
+  const int t0 = c * (int)p.Lc;
+  const int t1 = min(t0 + (int)p.Lc, L);
   const int N = (int)p.N;
 
   float Ap[NS];
@@ -71,23 +90,25 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
 #pragma unroll
     for (int n = 0; n < NS; ++n) h[n] = (n < N) ? hin[n] : 0.f;
   }
-  const float bias = p.has_bias ? p.bias[d * p.sbias] : 0.f;
+  const bool has_bias = p.has_bias != 0;
+  const float bias = has_bias ? p.bias[d * p.sbias] : 0.f;
   const float Dv = (FULL && p.has_D) ? p.Dp[d * p.sD] : 0.f;
-  const bool has_z = FULL && p.has_z;
+  constexpr bool has_z = HAS_Z;
   const bool softplus = p.softplus != 0;
+  float* const xck = (FULL && p.x_ckpt != nullptr && active) ? p.x_ckpt + ch * p.nck * p.N : nullptr;
 
   // Buffer resources based at (b, d0, t0) of each [batch, dim, seqlen] tensor.
-  const auto rs_u = make_rsrc((const char*)p.u + (b * p.su[0] + d0 * p.su[1] + t0 * p.su[2]) * ES);
-  const auto rs_d = make_rsrc((const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1] + t0 * p.sdl[2]) * ES);
+  const auto rs_u = make_rsrc((const char*)p.u + (b * p.su[0] + d0 * p.su[1] + (int64_t)t0 * p.su[2]) * ES);
+  const auto rs_d = make_rsrc((const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1] + (int64_t)t0 * p.sdl[2]) * ES);
   const uint32_t vo_u = active ? (uint32_t)(lane * p.su[1] * ES) : kOffDrop;
   const uint32_t vo_d = active ? (uint32_t)(lane * p.sdl[1] * ES) : kOffDrop;
   const uint32_t st_u = (uint32_t)(p.su[2] * ES), st_d = (uint32_t)(p.sdl[2] * ES);
   // Unused resources (no output in the summary pass, no z) point at u and are never read.
-  const auto rs_o = make_rsrc(FULL ? (const char*)p.out + (b * p.so[0] + d0 * p.so[1] + t0 * p.so[2]) * ES
+  const auto rs_o = make_rsrc(FULL ? (const char*)p.out + (b * p.so[0] + d0 * p.so[1] + (int64_t)t0 * p.so[2]) * ES
                                    : (const char*)p.u);
-  const auto rs_z = make_rsrc(has_z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1] + t0 * p.sz[2]) * ES
+  const auto rs_z = make_rsrc(has_z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1] + (int64_t)t0 * p.sz[2]) * ES
                                     : (const char*)p.u);
-  const auto rs_oz = make_rsrc(has_z ? (const char*)p.out_z + (b * p.soz[0] + d0 * p.soz[1] + t0 * p.soz[2]) * ES
+  const auto rs_oz = make_rsrc(has_z ? (const char*)p.out_z + (b * p.soz[0] + d0 * p.soz[1] + (int64_t)t0 * p.soz[2]) * ES
                                      : (const char*)p.u);
   const uint32_t vo_o = (FULL && active) ? (uint32_t)(lane * p.so[1] * ES) : kOffDrop;
   const uint32_t vo_z = (has_z && active) ? (uint32_t)(lane * p.sz[1] * ES) : kOffDrop;
@@ -95,10 +116,10 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const uint32_t st_o = FULL ? (uint32_t)(p.so[2] * ES) : 0u;
   const uint32_t st_z = has_z ? (uint32_t)(p.sz[2] * ES) : 0u;
   const uint32_t st_oz = has_z ? (uint32_t)(p.soz[2] * ES) : 0u;
-  const char* Brow = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + t0 * p.sB[3]) * Elem<Tbc>::kSize;
-  const char* Crow = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + t0 * p.sC[3]) * Elem<Tbc>::kSize;
-  const int64_t Bstep = p.sB[3] * Elem<Tbc>::kSize;
-  const int64_t Cstep = p.sC[3] * Elem<Tbc>::kSize;
+  // B / C rows of this wave's (batch, group), from step t0; 32-bit byte offsets per step.
+  const char* const Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3]) * EB;
+  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const uint32_t Bst = (uint32_t)(p.sB[3] * EB), Cst = (uint32_t)(p.sC[3] * EB);
 
   SeqCursor sc;
   if (VARLEN) sc = seq_cursor_at(p.cu, p.nseq, t0);
@@ -107,7 +128,7 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   // Register double buffer: the next block's u / delta / z are in flight while the
   // current block computes.  Loads past t1 re-read step t1 - 1.
   float un[TB], dn[TB], zn[TB];
-  auto fetch = [&](int64_t tb) {
+  auto fetch = [&](int tb) {
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
       const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
@@ -121,14 +142,11 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   // B_t / C_t arrive through the scalar cache one group of G states ahead of their use;
   // the scheduling barrier after each group keeps the compiler from hoisting every row of
   // the unrolled block into SGPRs at once.
-  constexpr int G = NS < 16 ? NS : 16;
-  constexpr int NG = NS / G;
-  constexpr int EB = Elem<Tbc>::kSize;
   BCGroup<Tbc> bnx, cnx;
-  bnx.template load<G>(Brow);
-  if (FULL) cnx.template load<G>(Crow);
+  bnx.template load<G>(Bbase);
+  if (FULL) cnx.template load<G>(Cbase);
 
-  for (int64_t tb = t0; tb < t1; tb += TB) {
+  for (int tb = t0; tb < t1; tb += TB) {
     float uc[TB], dc[TB], zc[TB];
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
@@ -139,7 +157,7 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
     if (tb + TB < t1) fetch(tb + TB);
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-      const int64_t t = tb + i;
+      const int t = tb + i;
       if (t < t1) {
         if (VARLEN && t == sc.pending) {
 #pragma unroll
@@ -151,7 +169,8 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
         const uint32_t r = (uint32_t)(t - t0);
         const uint32_t rn = (uint32_t)(min(t + 1, t1 - 1) - t0);
         const float uu = uc[i];
-        float dt = dc[i] + bias;
+        float dt = dc[i];
+        if (has_bias) dt += bias;
         if (softplus) dt = softplus20(dt);
         const float dtu = dt * uu;
         // y accumulates in 4 independent FMA chains (n mod 4): shorter dependency chains
@@ -162,18 +181,19 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
           const BCGroup<Tbc> bcur = bnx;
           BCGroup<Tbc> ccur;
           if (FULL) ccur = cnx;
-          const int64_t off_b = (gi + 1 < NG) ? ((int64_t)r * Bstep + (gi + 1) * G * EB) : (int64_t)rn * Bstep;
-          bnx.template load<G>(Brow + off_b);
-          if (FULL) {
-            const int64_t off_c = (gi + 1 < NG) ? ((int64_t)r * Cstep + (gi + 1) * G * EB) : (int64_t)rn * Cstep;
-            cnx.template load<G>(Crow + off_c);
+          if (gi + 1 < NG) {
+            bnx.template load<G>(Bbase + r * Bst + (gi + 1) * G * EB);
+            if (FULL) cnx.template load<G>(Cbase + r * Cst + (gi + 1) * G * EB);
+          } else {
+            bnx.template load<G>(Bbase + rn * Bst);
+            if (FULL) cnx.template load<G>(Cbase + rn * Cst);
           }
 #pragma unroll
           for (int k = 0; k < G; ++k) {
             const int n = gi * G + k;
             const float a = fast_exp2(dt * Ap[n]);
             h[n] = fmaf(a, h[n], dtu * bcur.get(k));
-            if (FULL) ys[k & 3] = fmaf(ccur.get(k), h[n], ys[k & 3]);
+            if (FULL) ys[k & 3] = (gi == 0 && k < 4) ? ccur.get(k) * h[n] : fmaf(ccur.get(k), h[n], ys[k & 3]);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -187,35 +207,19 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
             const float zz = zc[i];
             Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
           }
-          if (VARLEN && p.last_state != nullptr && active && (t + 1 == sc.pending || t == p.L - 1)) {
-            float* ls = p.last_state + ((int64_t)(sc.idx - 1) * p.D + d) * p.N;
-#pragma unroll
-            for (int n = 0; n < NS; ++n)
-              if (n < N) ls[n] = h[n];
-          }
-          if (((t + 1) % kCk == 0 || t == p.L - 1) && active) {
-            if (p.x_ckpt != nullptr) {
-              float* xc = p.x_ckpt + (ch * p.nck + t / kCk) * p.N;
-#pragma unroll
-              for (int n = 0; n < NS; ++n)
-                if (n < N) xc[n] = h[n];
-            }
-            if (!VARLEN && p.last_state != nullptr && t == p.L - 1) {
-              float* ls = p.last_state + ch * p.N;
-#pragma unroll
-              for (int n = 0; n < NS; ++n)
-                if (n < N) ls[n] = h[n];
-            }
+          if (VARLEN && p.last_state != nullptr && active && (t + 1 == sc.pending || t == L - 1))
+            store_state<NS>(p.last_state + ((int64_t)(sc.idx - 1) * p.D + d) * p.N, h, N);
+          if (((t + 1) & (kCk - 1)) == 0 || t == L - 1) {
+            if (xck != nullptr) store_state<NS>(xck + (int64_t)(t / kCk) * p.N, h, N);
+            if (!VARLEN && p.last_state != nullptr && active && t == L - 1)
+              store_state<NS>(p.last_state + ch * p.N, h, N);
           }
         }
       }
     }
   }
   if (!FULL && active) {
-    float* ho = p.ws_h + (ch * p.K + c) * p.N;
-#pragma unroll
-    for (int n = 0; n < NS; ++n)
-      if (n < N) ho[n] = h[n];
+    store_state<NS>(p.ws_h + (ch * p.K + c) * p.N, h, N);
     p.ws_s[ch * p.K + c] = ssum;
   }
 }
@@ -287,7 +291,7 @@ static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st, void* const* e
   hipError_t e = hipSuccess;
   if (k.K > 1) {
     dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)(k.K - 1));
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, false, VARLEN>), grid, dim3(kWave), 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 0, VARLEN>), grid, dim3(kWave), 0, st, k);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t total = k.Bsz * k.D * k.N;
@@ -298,7 +302,10 @@ static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st, void* const* e
   dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)k.K);
   e = record(ev, 0, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, true, VARLEN>), grid, dim3(kWave), 0, st, k);
+  if (k.has_z)
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 2, VARLEN>), grid, dim3(kWave), 0, st, k);
+  else
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 1, VARLEN>), grid, dim3(kWave), 0, st, k);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return record(ev, 1, st);
