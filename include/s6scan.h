@@ -19,10 +19,13 @@
  *   A                                              : [dim, dstate] fp32, any strides
  *   B, C, dB, dC                                   : [batch, ngroups, dstate, seqlen], any strides
  *   D, delta_bias, dD, ddelta_bias                 : [dim] fp32, any stride
- *   x_ckpt                                         : [batch, dim, s6_num_checkpoints(), dstate] fp32,
- *                                                    contiguous; entry k is the state after
- *                                                    step min((k+1)*S6_CKPT_INTERVAL, seqlen)-1,
- *                                                    so entry [-1] is the final state.
+ *   x_ckpt                                         : [batch, s6_num_checkpoints(), dim, dstate]
+ *                                                    fp32, contiguous; entry k is the state
+ *                                                    after step min((k+1)*S6_CKPT_INTERVAL,
+ *                                                    seqlen)-1, so x_ckpt[:, -1] is the final
+ *                                                    state.  It plays the role of the
+ *                                                    reference kernel's saved `x`
+ *                                                    (selective_scan_interface.py:42-47).
  *   last_state                                     : [batch, dim, dstate] fp32 contiguous
  *                                                    ([nseq, dim, dstate] for varlen)
  *   Varlen (nseq > 0): batch == 1, cu_seqlens is a device int32 [nseq+1] with
@@ -46,8 +49,8 @@
 extern "C" {
 #endif
 
-#define S6_ABI_VERSION 1
-#define S6_CKPT_INTERVAL 32   /* steps between saved states in x_ckpt */
+#define S6_ABI_VERSION 2
+#define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
 #define S6_MAX_DSTATE_BWD 16
 

@@ -15,7 +15,12 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "s6scan", "libs6scan.so")
-SOURCES = ["s6_abi.cpp", "s6_fwd.hip", "s6_bwd.hip"]
+# (source, object name, extra defines): the scan kernels are compiled once per input
+# dtype so the translation units build in parallel.
+_TIO = {"f32": "float", "bf16": "s6::bf16", "f16": "s6::f16"}
+UNITS = [("s6_abi.cpp", "s6_abi", []), ("s6_misc.hip", "s6_misc", [])]
+UNITS += [(f"s6_{d}.hip", f"s6_{d}_{t}", [f"-DS6_TIO={ty}"])
+          for d in ("fwd", "bwd") for t, ty in _TIO.items()]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -27,9 +32,10 @@ CFLAGS = [
 ]
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(unit):
+    src, name, defs = unit
+    obj = os.path.join(BUILD, name + ".o")
+    cmd = [HIPCC, *CFLAGS, *defs, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
@@ -38,8 +44,8 @@ def _compile(src):
 
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    with ThreadPoolExecutor(max_workers=min(len(UNITS), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(_compile, UNITS))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -35,18 +35,19 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int esize(int dt) { return dt == S6_F32 ? 4 : 2; }
 
 struct Plan {
-  int64_t Dg, nJ64, nJ256, nDblk64;
+  int64_t Dg, nJ, nDblk;
   int64_t K, Lc, nck;
   bool relayout_B, relayout_C;
   int64_t NP;  // padded dstate of relaid-out B / C
-  size_t off_h, off_s, off_B, off_C, off_pB, off_pC, total_fwd, total_bwd;
+  size_t off_h, off_s, off_r, off_B, off_C, total_fwd;
+  size_t off_pB, off_pC, off_dA, off_dD, off_db, total_bwd;
 };
 
 // States held per lane by the kernels: the forward pads dstate to 8/16/32/64, the backward
-// to 16.  B and C rows are read as NS contiguous values, so a row is used in place only
+// to 8/16.  B and C rows are read as NS contiguous values, so a row is used in place only
 // when dstate == NS, the state axis is contiguous and 16-bit rows are 4-byte aligned.
 int64_t ns_fwd(int64_t N) { return N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
-int64_t ns_bwd(int64_t) { return 16; }
+int64_t ns_bwd(int64_t N) { return N <= 8 ? 8 : 16; }
 
 bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_t NS) {
   if (N != NS || s[2] != 1) return false;
@@ -57,15 +58,14 @@ bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_
 }
 
 // Chunking and workspace layout; ptrs may be null (sizing only, then relayout is assumed
-// to be needed exactly when the strides say so).
+// to be needed).
 Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, const void* Cp,
                const int64_t* sC) {
   Plan pl{};
   pl.Dg = p.dim / p.ngroups;
-  pl.nJ64 = ceil_div(pl.Dg, 64);
-  pl.nJ256 = ceil_div(pl.Dg, 256);
-  pl.nDblk64 = p.ngroups * pl.nJ64;
-  const int64_t chw = p.batch * pl.nDblk64;
+  pl.nJ = ceil_div(pl.Dg, 64);
+  pl.nDblk = p.ngroups * pl.nJ;
+  const int64_t chw = p.batch * pl.nDblk;
   const int64_t ktarget = ceil_div(kTargetWaves, chw > 0 ? chw : 1);
   int64_t Lc = ceil_div(p.seqlen, ktarget > 0 ? ktarget : 1);
   if (Lc < kMinChunk) Lc = kMinChunk;
@@ -74,7 +74,6 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   pl.K = ceil_div(p.seqlen, Lc);
   pl.nck = ceil_div(p.seqlen, s6::kCk);
   const int64_t NS = bwd ? ns_bwd(p.dstate) : ns_fwd(p.dstate);
-  // Without pointers (sizing queries) assume the worst case: both B and C relaid out.
   pl.relayout_B = sB ? !bc_scalar_ok(Bp, sB, p.bc_dtype, p.dstate, NS) : true;
   pl.relayout_C = sC ? !bc_scalar_ok(Cp, sC, p.bc_dtype, p.dstate, NS) : true;
   pl.NP = NS;
@@ -84,17 +83,26 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   off += pl.K > 1 ? align256(nchan * pl.K * p.dstate * 4) : 0;
   pl.off_s = off;
   off += pl.K > 1 ? align256(nchan * pl.K * 4) : 0;
+  pl.off_r = off;
+  off += (pl.K > 1 && p.nseq > 0) ? align256(nchan * pl.K * 4) : 0;
   const size_t bc_bytes = align256((size_t)(p.batch * p.ngroups * p.seqlen * pl.NP) * esize(p.bc_dtype));
   pl.off_B = off;
   off += pl.relayout_B ? bc_bytes : 0;
   pl.off_C = off;
   off += pl.relayout_C ? bc_bytes : 0;
   pl.total_fwd = off;
-  const size_t part = align256((size_t)(p.batch * p.ngroups * pl.nJ256 * p.seqlen * p.dstate) * 4);
+  const size_t part = align256((size_t)(p.batch * p.ngroups * pl.nJ * p.seqlen * s6::kPartRow) * 4);
   pl.off_pB = off;
   off += part;
   pl.off_pC = off;
   off += part;
+  const size_t rows = (size_t)(p.batch * pl.K);
+  pl.off_dA = off;
+  off += align256(rows * p.dim * p.dstate * 4);
+  pl.off_dD = off;
+  off += p.has_D ? align256(rows * p.dim * 4) : 0;
+  pl.off_db = off;
+  off += p.has_delta_bias ? align256(rows * p.dim * 4) : 0;
   pl.total_bwd = off;
   return pl;
 }
@@ -179,10 +187,10 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   k.x_ckpt = a.x_ckpt; k.nck = pl.nck; k.last_state = a.last_state;
   k.ws_h = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
   k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;
-  k.ws_r = nullptr;
+  k.ws_r = (pl.K > 1 && p.nseq > 0) ? (int32_t*)(ws + pl.off_r) : nullptr;
   k.K = pl.K; k.Lc = pl.Lc;
   k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
-  k.nDblk = pl.nDblk64;
+  k.nDblk = pl.nDblk;
   return k;
 }
 
@@ -280,6 +288,13 @@ int s6_validate_bwd(const S6BwdArgs* a) {
     return r;
   if (p.has_delta_bias && (r = check_ptr(a->ddelta_bias, "ddelta_bias"))) return r;
   const Plan pl = make_plan(p, true, a->B, a->B_stride, a->C, a->C_stride);
+  const int es = esize(p.io_dtype);
+  if ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
+      (r = check_span(a->dout_stride, es, pl.Lc, "dout")) || (r = check_span(a->du_stride, es, pl.Lc, "du")) ||
+      (r = check_span(a->ddelta_stride, es, pl.Lc, "ddelta")) ||
+      (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
+                   (r = check_span(a->dz_stride, es, pl.Lc, "dz")))))
+    return r;
   if (pl.total_bwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_bwd))
     return fail(S6_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", pl.total_bwd,
                 a->workspace ? a->workspace_bytes : (size_t)0);
@@ -324,20 +339,6 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
   if (e == hipSuccess && pl.relayout_C)
     e = s6::launch_relayout(a->C, a->C_stride, esize(p.bc_dtype), ws + pl.off_C, p.batch,
                             p.ngroups, p.dstate, pl.NP, p.seqlen, st);
-  // dA, dD and ddelta_bias are accumulated with atomics: clear them first (fill kernels,
-  // not memset nodes, so the sequence stays valid inside a captured graph).
-  if (e == hipSuccess && a->dA_stride[1] == 1 && a->dA_stride[0] == p.dstate)
-    e = s6::launch_fill(a->dA, p.dim * p.dstate, 0.f, st);
-  else if (e == hipSuccess)
-    return fail(S6_E_INVALID, "dA must be a contiguous [dim, dstate] fp32 tensor");
-  if (e == hipSuccess && p.has_D) {
-    if (a->dD_stride != 1) return fail(S6_E_INVALID, "dD must be contiguous");
-    e = s6::launch_fill(a->dD, p.dim, 0.f, st);
-  }
-  if (e == hipSuccess && p.has_delta_bias) {
-    if (a->ddelta_bias_stride != 1) return fail(S6_E_INVALID, "ddelta_bias must be contiguous");
-    e = s6::launch_fill(a->ddelta_bias, p.dim, 0.f, st);
-  }
   if (e == hipSuccess) {
     s6::BwdK k{};
     k.Bsz = p.batch; k.D = p.dim; k.L = p.seqlen; k.N = p.dstate; k.G = p.ngroups;
@@ -377,10 +378,14 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.dA = a->dA; k.dD = a->dD; k.dbias = a->ddelta_bias; k.dB = a->dB; k.dC = a->dC;
     k.ws_g = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
     k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;
+    k.ws_r = (pl.K > 1 && p.nseq > 0) ? (int32_t*)(ws + pl.off_r) : nullptr;
     k.ws_pB = (float*)(ws + pl.off_pB);
     k.ws_pC = (float*)(ws + pl.off_pC);
+    k.ws_dA = (float*)(ws + pl.off_dA);
+    k.ws_dD = p.has_D ? (float*)(ws + pl.off_dD) : nullptr;
+    k.ws_db = p.has_delta_bias ? (float*)(ws + pl.off_db) : nullptr;
     k.K = pl.K; k.Lc = pl.Lc;
-    k.nDblk = pl.nDblk64; k.nJ4 = pl.nJ256;
+    k.nDblk = pl.nDblk; k.nJ = pl.nJ;
     k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
     e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st, a->kernel_events);
   }

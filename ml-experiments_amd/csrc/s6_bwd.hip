@@ -1,81 +1,55 @@
 // Backward S6 selective scan for gfx950.
 //
-// With lambda_t = dL/dh_t and g_t = abar_t * lambda_t (the gradient that step t passes to
-// h_{t-1}):
+// With lambda_t = dL/dh_t and g_t = abar_t lambda_t (the gradient step t passes to h_{t-1}):
 //     lambda_t = C_t dy_t + g_{t+1},     g_t = abar_t lambda_t   (g_t = 0 at a sequence start)
 //     q_t = abar_t h_{t-1} lambda_t   (gradient of the exponent Delta_t A)
 //     dA += q Delta,  dDelta = sum_n q A + u sum_n lambda B,  du = Delta sum_n lambda B + D dy
 //     dB_t += lambda Delta u,  dC_t += dy h_t        (summed over the channels of a group)
-// These are the gradients autograd produces through selective_scan_ref
-// (selective_scan_interface.py:107-156); the reference's native bwd is replaced here.
+// where dy is dout, times silu(z) when z is given.  These are the gradients autograd
+// produces through selective_scan_ref (selective_scan_interface.py:107-156); they replace
+// the reference's native bwd (selective_scan_interface.py:67-70).
 //
-// Kernels (the reverse mirror of the forward's chunking):
-//   bwd_summary  per chunk c >= 1: g leaving the chunk at its first step, from a zero
-//                inflow, and the chunk's sum of Delta.
-//   bwd_carry    reverse prefix over chunks: g entering each chunk.
-//   bwd_main     per chunk, per 32-step checkpoint interval (in reverse): reload the state
-//                saved by the forward, recompute 8-step segments forward into registers,
-//                then run the reverse recurrence.  dB/dC are reduced over the 64 lanes of a
-//                wave with permlane swaps and DPP, then over the 4 waves of the workgroup in
-//                LDS, and written as one partial per 256-channel block (deterministic).
-//   bwd_reduce_bc  sums the partials into dB / dC.
+// Kernels (the reverse mirror of the forward's chunking; lane = channel, 64 per wave):
+//   bwd_summary  per chunk c >= 1: the gradient leaving the chunk at its first step from a
+//                zero inflow, and the chunk's sum of Delta.
+//   bwd_carry    reverse segmented scan over chunks (s6_misc.hip): gradient entering each chunk.
+//   bwd_scan     per chunk, per 8-step segment in reverse: the state saved by the forward at
+//                the segment start, a forward recompute of the segment into registers, then
+//                the reverse recurrence.  States are processed 8 at a time (two halves for
+//                dstate 16) so the segment's states fit in VGPRs.  dB / dC are reduced over the
+//                64 lanes with permlane swaps and DPP and written as one partial per wave;
+//                dA / dD / ddelta_bias as one partial per (batch, chunk).
+//   bwd_reduce_* fixed-order sums of the partials (s6_misc.hip): the result is deterministic.
+#include <type_traits>
+
 #include "s6_internal.h"
 #include "s6_wave.h"
 
 namespace s6 {
 
-namespace {
-
-__device__ inline int64_t last_start_le(const int32_t* cu, int32_t nseq, int64_t t) {
-  int32_t lo = 0, hi = nseq + 1;  // first i with cu[i] > t
-  while (lo < hi) {
-    int32_t mid = (lo + hi) >> 1;
-    if ((int64_t)cu[mid] <= t) lo = mid + 1; else hi = mid;
-  }
-  return (lo > 0) ? (int64_t)cu[lo - 1] : -1;
-}
-
-// Bit i set when a sequence starts at step ts + i, for i in [0, te - ts) (te - ts <= 32).
-__device__ inline uint32_t start_mask(const int32_t* cu, int32_t nseq, int64_t ts, int64_t te) {
-  int32_t lo = 0, hi = nseq + 1;  // first i with cu[i] >= ts
-  while (lo < hi) {
-    int32_t mid = (lo + hi) >> 1;
-    if ((int64_t)cu[mid] < ts) lo = mid + 1; else hi = mid;
-  }
-  uint32_t m = 0;
-  for (int32_t i = lo; i <= nseq && (int64_t)cu[i] < te; ++i) m |= 1u << (uint32_t)(cu[i] - ts);
-  return m;
-}
-
-__device__ inline bool chunk_has_start(const int32_t* cu, int32_t nseq, int64_t t0, int64_t t1) {
-  int32_t lo = 0, hi = nseq + 1;
-  while (lo < hi) {
-    int32_t mid = (lo + hi) >> 1;
-    if ((int64_t)cu[mid] < t0) lo = mid + 1; else hi = mid;
-  }
-  return lo <= nseq && (int64_t)cu[lo] < t1;
-}
-
-}  // namespace
-
-template <typename Tio, typename Tbc, int NS, bool VARLEN>
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
 __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
+  constexpr int TB = kCk;
+  constexpr int ES = Elem<Tio>::kSize;
+  constexpr int EB = Elem<Tbc>::kSize;
+  constexpr int GS = NS < kGroupStates<Tbc> ? NS : kGroupStates<Tbc>;
+  constexpr int NG = NS / GS;
   const int lane = threadIdx.x;
+  const BlockPos bp = block_pos(p.Bsz * p.nDblk);
   const int64_t Dg = p.D / p.G;
-  const int64_t nJ = (Dg + kWave - 1) / kWave;
-  const int64_t blk = blockIdx.x;
-  const int64_t b = blk / p.nDblk;
-  const int64_t rem = blk % p.nDblk;
-  const int64_t g = rem / nJ;
-  const int64_t j = rem % nJ;
+  const int64_t b = bp.x / p.nDblk;
+  const int64_t rem = bp.x % p.nDblk;
+  const int64_t g = rem / p.nJ;
+  const int64_t j = rem % p.nJ;
   const int64_t dloc = j * kWave + lane;
   const bool active = dloc < Dg;
+  const int64_t d0 = g * Dg + j * kWave;
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int64_t c = blockIdx.y + 1;
-  const int64_t t0 = c * p.Lc;
-  const int64_t t1 = min(t0 + p.Lc, p.L);
+  const int c = (int)bp.y + 1;
+  const int t0 = c * (int)p.Lc;
+  const int t1 = min(t0 + (int)p.Lc, (int)p.L);
   const int N = (int)p.N;
-  const int64_t ch = b * p.D + d;
+  const bool varlen = p.nseq > 0;
 
   float Ap[NS], gs[NS];
 #pragma unroll
@@ -83,90 +57,115 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
     Ap[n] = (n < N) ? p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e : 0.f;
     gs[n] = 0.f;
   }
-  const float bias = p.has_bias ? p.bias[d * p.sbias] : 0.f;
-  const int64_t ub = b * p.sdl[0] + d * p.sdl[1];
-  const int64_t zb = b * p.sz[0] + d * p.sz[1];
-  const int64_t dob = b * p.sdo[0] + d * p.sdo[1];
-  const char* Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1]) * Elem<Tbc>::kSize;
-  const int64_t Cstep = p.sC[3] * Elem<Tbc>::kSize;
-  int64_t ps = VARLEN ? last_start_le(p.cu, p.nseq, t1 - 1) : -1;
-  float ssum = 0.f;
-  for (int64_t t = t1 - 1; t >= t0; --t) {
-    float Cv[NS];
-    BCLoad<Tbc>::template row<NS>(Cbase + t * Cstep, Cv);
-    float dy = Elem<Tio>::load(p.dout, dob + t * p.sdo[2]);
-    if (p.has_z) {
-      const float zz = Elem<Tio>::load(p.z, zb + t * p.sz[2]);
-      dy *= zz * sigmoidf_(zz);
-    }
-    float dt = Elem<Tio>::load(p.delta, ub + t * p.sdl[2]) + bias;
-    if (p.softplus) dt = softplus20(dt);
-    const bool st = VARLEN && t == ps;
+  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
+  const auto rs_o = make_rsrc((const char*)p.dout + (b * p.sdo[0] + d0 * p.sdo[1] + (int64_t)t0 * p.sdo[2]) * ES);
+  const auto rs_d = make_rsrc((const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1] + (int64_t)t0 * p.sdl[2]) * ES);
+  const auto rs_z = make_rsrc(HAS_Z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1] + (int64_t)t0 * p.sz[2]) * ES
+                                    : (const char*)p.dout);
+  const uint32_t vo_o = active ? (uint32_t)(lane * p.sdo[1] * ES) : kOffDrop;
+  const uint32_t vo_d = active ? (uint32_t)(lane * p.sdl[1] * ES) : kOffDrop;
+  const uint32_t vo_z = (HAS_Z && active) ? (uint32_t)(lane * p.sz[1] * ES) : kOffDrop;
+  const uint32_t st_o = (uint32_t)(p.sdo[2] * ES), st_d = (uint32_t)(p.sdl[2] * ES);
+  const uint32_t st_z = HAS_Z ? (uint32_t)(p.sz[2] * ES) : 0u;
+  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const uint32_t Cst = (uint32_t)(p.sC[3] * EB);
+
+  float on[TB], dn[TB], zn[TB];
+  auto fetch = [&](int tb) {
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      const float lam = fmaf(Cv[n], dy, gs[n]);
-      const float a = fast_exp2(dt * Ap[n]);
-      gs[n] = st ? 0.f : a * lam;
+    for (int i = 0; i < TB; ++i) {
+      const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
+      on[i] = Buf<Tio>::load(rs_o, vo_o, r * st_o);
+      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
+      if (HAS_Z) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
     }
-    ssum += dt;
-    if (st) ps = last_start_le(p.cu, p.nseq, t - 1);
+  };
+  const int tlast = t0 + ((t1 - 1 - t0) / TB) * TB;  // first step of the last block
+  fetch(tlast);
+  BCGroup<Tbc> cnx;
+  cnx.template load<GS>(Cbase + (uint32_t)(t1 - 1 - t0) * Cst);
+  float ssum = 0.f;
+  bool seen_start = false;  // a sequence starts inside this chunk
+
+  for (int tb = tlast; tb >= t0; tb -= TB) {
+    float oc[TB], dc[TB], zc[TB];
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+      oc[i] = on[i];
+      dc[i] = dn[i];
+      zc[i] = HAS_Z ? zn[i] : 0.f;
+    }
+    if (tb > t0) fetch(tb - TB);
+    const uint32_t smask = varlen ? start_mask(p.cu, p.nseq, tb, min(tb + TB, t1)) : 0u;
+    seen_start = seen_start || smask != 0u;
+#pragma unroll
+    for (int i = TB - 1; i >= 0; --i) {
+      const int t = tb + i;
+      if (t < t1) {
+        float dy = oc[i];
+        if (HAS_Z) dy *= zc[i] * sigmoidf_(zc[i]);
+        const float dt = prep_dt<DTM>(dc[i], bias);
+        const uint32_t r = (uint32_t)(t - t0);
+        const uint32_t rn = (uint32_t)(max(t - 1, t0) - t0);
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          cnx.touch();
+          const BCGroup<Tbc> ccur = cnx;
+          cnx.template load<GS>(Cbase + opaque(gi + 1 < NG ? r * Cst + (uint32_t)((gi + 1) * GS * EB)
+                                                            : rn * Cst));
+          // A sequence start at t cuts the flow into the previous sequence (g_t = 0); the
+          // uniform branch keeps the common case free of per-state selects.
+          auto body = [&](auto st_tag) {
+            constexpr bool ST = decltype(st_tag)::value;
+#pragma unroll
+            for (int k = 0; k < GS; ++k) {
+              const int n = gi * GS + k;
+              const float lam = fmaf(ccur.get(k), dy, gs[n]);
+              gs[n] = ST ? 0.f : fast_exp2(dt * Ap[n]) * lam;
+            }
+          };
+          if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
+        }
+        ssum += dt;
+      }
+    }
   }
   if (active) {
+    const int64_t ch = b * p.D + d;
     float* go = p.ws_g + (ch * p.K + c) * p.N;
 #pragma unroll
     for (int n = 0; n < NS; ++n)
       if (n < N) go[n] = gs[n];
     p.ws_s[ch * p.K + c] = ssum;
+    if (varlen) p.ws_r[ch * p.K + c] = seen_start ? 1 : 0;
   }
 }
 
-__global__ void __launch_bounds__(256) bwd_carry(BwdK p) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = p.Bsz * p.D * p.N;
-  if (i >= total) return;
-  const int64_t ch = i / p.N;
-  const int64_t n = i % p.N;
-  const int64_t d = ch % p.D;
-  const float ap = p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e;
-  float gin = 0.f;
-  for (int64_t c = p.K - 1; c >= 0; --c) {
-    float* slot = p.ws_g + (ch * p.K + c) * p.N + n;
-    const float gloc = (c >= 1) ? *slot : 0.f;
-    *slot = gin;
-    if (c >= 1) {
-      const int64_t t0 = c * p.Lc, t1 = min(t0 + p.Lc, p.L);
-      const bool reset = p.nseq > 0 && chunk_has_start(p.cu, p.nseq, t0, t1);
-      const float decay = fast_exp2(ap * p.ws_s[ch * p.K + c]);
-      gin = (reset ? 0.f : decay * gin) + gloc;
-    }
-  }
-}
-
-template <typename Tio, typename Tbc, bool VARLEN>
-__global__ void __launch_bounds__(256) bwd_main(BwdK p) {
-  constexpr int NS = 16;
-  constexpr int SEG = 8;
-  constexpr int NSEG = kCk / SEG;
-  __shared__ float s_seg[NSEG][NS][256];   // state at the start of each segment
-  __shared__ float s_red[2][SEG][4][NS];   // per-wave dB / dC sums for one segment
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = tid >> 6;
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+__global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_scan(BwdK p) {
+  constexpr int SEG = kCk;  // steps per segment = checkpoint interval
+  constexpr int HS = 8;     // states per half
+  constexpr int NH = NS / HS;
+  static_assert(NS % HS == 0, "dstate padding");
+  constexpr int ES = Elem<Tio>::kSize;
+  constexpr int EB = Elem<Tbc>::kSize;
+  const int lane = threadIdx.x;
+  const BlockPos bp = block_pos(p.Bsz * p.nDblk);
   const int64_t Dg = p.D / p.G;
-  const int64_t blk = blockIdx.x;
-  const int64_t b = blk / (p.G * p.nJ4);
-  const int64_t rem = blk % (p.G * p.nJ4);
-  const int64_t g = rem / p.nJ4;
-  const int64_t j4 = rem % p.nJ4;
-  const int64_t dloc = j4 * 256 + tid;
+  const int64_t b = bp.x / p.nDblk;
+  const int64_t rem = bp.x % p.nDblk;
+  const int64_t g = rem / p.nJ;
+  const int64_t j = rem % p.nJ;
+  const int64_t dloc = j * kWave + lane;
   const bool active = dloc < Dg;
+  const int64_t d0 = g * Dg + j * kWave;
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int64_t c = blockIdx.y;
-  const int64_t t0 = c * p.Lc;
-  const int64_t t1 = min(t0 + p.Lc, p.L);
+  const int c = (int)bp.y;
+  const int t0 = c * (int)p.Lc;
+  const int t1 = min(t0 + (int)p.Lc, (int)p.L);
   const int N = (int)p.N;
   const int64_t ch = b * p.D + d;
+  const bool varlen = p.nseq > 0;
 
   float Ap[NS], gs[NS], dAacc[NS];
   {
@@ -178,249 +177,255 @@ __global__ void __launch_bounds__(256) bwd_main(BwdK p) {
       dAacc[n] = 0.f;
     }
   }
-  const float bias = p.has_bias ? p.bias[d * p.sbias] : 0.f;
+  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
   const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
   float dDacc = 0.f, dbacc = 0.f;
 
-  const int64_t ub = b * p.su[0] + d * p.su[1];
-  const int64_t db = b * p.sdl[0] + d * p.sdl[1];
-  const int64_t zb = b * p.sz[0] + d * p.sz[1];
-  const int64_t dob = b * p.sdo[0] + d * p.sdo[1];
-  const int64_t oub = b * p.sout[0] + d * p.sout[1];
-  const int64_t dub = b * p.sdu[0] + d * p.sdu[1];
-  const int64_t ddb = b * p.sddl[0] + d * p.sddl[1];
-  const int64_t dzb = b * p.sdz[0] + d * p.sdz[1];
-  const char* Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1]) * Elem<Tbc>::kSize;
-  const char* Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1]) * Elem<Tbc>::kSize;
-  const int64_t Bstep = p.sB[3] * Elem<Tbc>::kSize;
-  const int64_t Cstep = p.sC[3] * Elem<Tbc>::kSize;
-  float* pBrow = p.ws_pB + ((b * p.G + g) * p.nJ4 + j4) * p.L * p.N;
-  float* pCrow = p.ws_pC + ((b * p.G + g) * p.nJ4 + j4) * p.L * p.N;
+  // Buffer resources based at (b, d0, t0); inactive lanes load 0 and drop their stores.
+  auto rsrc = [&](const void* base, const int64_t* s) {
+    return make_rsrc((const char*)base + (b * s[0] + d0 * s[1] + (int64_t)t0 * s[2]) * ES);
+  };
+  const auto rs_u = rsrc(p.u, p.su), rs_d = rsrc(p.delta, p.sdl), rs_o = rsrc(p.dout, p.sdo);
+  const auto rs_du = rsrc(p.du, p.sdu), rs_dd = rsrc(p.ddelta, p.sddl);
+  const auto rs_z = rsrc(HAS_Z ? p.z : p.u, HAS_Z ? p.sz : p.su);
+  const auto rs_y = rsrc(HAS_Z ? p.out : p.u, HAS_Z ? p.sout : p.su);
+  const auto rs_dz = rsrc(HAS_Z ? p.dz : p.du, HAS_Z ? p.sdz : p.sdu);
+  auto voff = [&](const int64_t* s, bool on) {
+    return (on && active) ? (uint32_t)(lane * s[1] * ES) : kOffDrop;
+  };
+  const uint32_t vo_u = voff(p.su, true), vo_d = voff(p.sdl, true), vo_o = voff(p.sdo, true);
+  const uint32_t vo_du = voff(p.sdu, true), vo_dd = voff(p.sddl, true);
+  const uint32_t vo_z = voff(p.sz, HAS_Z), vo_y = voff(p.sout, HAS_Z), vo_dz = voff(p.sdz, HAS_Z);
+  const uint32_t st_u = (uint32_t)(p.su[2] * ES), st_d = (uint32_t)(p.sdl[2] * ES);
+  const uint32_t st_o = (uint32_t)(p.sdo[2] * ES);
+  const uint32_t st_du = (uint32_t)(p.sdu[2] * ES), st_dd = (uint32_t)(p.sddl[2] * ES);
+  const uint32_t st_z = HAS_Z ? (uint32_t)(p.sz[2] * ES) : 0u;
+  const uint32_t st_y = HAS_Z ? (uint32_t)(p.sout[2] * ES) : 0u;
+  const uint32_t st_dz = HAS_Z ? (uint32_t)(p.sdz[2] * ES) : 0u;
 
-  const int64_t nsub = (t1 - t0 + kCk - 1) / kCk;
-  for (int64_t s = nsub - 1; s >= 0; --s) {
-    const int64_t ts = t0 + s * kCk;
-    const int64_t te = min(ts + kCk, t1);
-    const uint32_t smask = VARLEN ? start_mask(p.cu, p.nseq, ts, te) : 0u;
-    float h[NS];
-    if (ts == 0) {
+  const char* const Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3]) * EB;
+  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const uint32_t Bst = (uint32_t)(p.sB[3] * EB), Cst = (uint32_t)(p.sC[3] * EB);
+  float* const pBrow = p.ws_pB + ((b * p.G + g) * p.nJ + j) * p.L * kPartRow;
+  float* const pCrow = p.ws_pC + ((b * p.G + g) * p.nJ + j) * p.L * kPartRow;
+  const float* const xck = p.x_ckpt + (b * p.nck * p.D + d) * p.N;  // [b, k, d, :]
+  const int64_t xck_step = p.D * p.N;
+
+  // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
+  // while the current one computes.
+  float un[SEG], dn[SEG], on[SEG], zn[SEG], yn[SEG], hn[NS];
+  auto fetch = [&](int ts) {
+    const int te = min(ts + SEG, t1);
 #pragma unroll
-      for (int n = 0; n < NS; ++n) h[n] = 0.f;
-    } else {
-      const float* xc = p.x_ckpt + (ch * p.nck + ts / kCk - 1) * p.N;
-#pragma unroll
-      for (int n = 0; n < NS; ++n) h[n] = (n < N) ? xc[n] : 0.f;
-    }
-    // Pre-pass: states at the segment starts.
-    for (int k = 0; k < NSEG; ++k) {
-#pragma unroll
-      for (int n = 0; n < NS; ++n) s_seg[k][n][tid] = h[n];
-      const int64_t sg0 = ts + k * SEG;
-#pragma unroll
-      for (int i = 0; i < SEG; ++i) {
-        const int64_t t = sg0 + i;
-        if (t < te) {
-          if (VARLEN && ((smask >> (uint32_t)(t - ts)) & 1u)) {
-#pragma unroll
-            for (int n = 0; n < NS; ++n) h[n] = 0.f;
-          }
-          float Bv[NS];
-          BCLoad<Tbc>::template row<NS>(Bbase + t * Bstep, Bv);
-          const float uu = Elem<Tio>::load(p.u, ub + t * p.su[2]);
-          float dt = Elem<Tio>::load(p.delta, db + t * p.sdl[2]) + bias;
-          if (p.softplus) dt = softplus20(dt);
-          const float dtu = dt * uu;
-#pragma unroll
-          for (int n = 0; n < NS; ++n) h[n] = fmaf(fast_exp2(dt * Ap[n]), h[n], dtu * Bv[n]);
-        }
+    for (int i = 0; i < SEG; ++i) {
+      const uint32_t r = (uint32_t)(min(ts + i, te - 1) - t0);
+      un[i] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
+      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
+      on[i] = Buf<Tio>::load(rs_o, vo_o, r * st_o);
+      if (HAS_Z) {
+        zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
+        yn[i] = Buf<Tio>::load(rs_y, vo_y, r * st_y);
       }
     }
-    // Reverse over segments.
-    for (int k = NSEG - 1; k >= 0; --k) {
-      const int64_t sg0 = ts + k * SEG;
-      if (sg0 >= te) continue;
-      float hs[SEG][NS];
-      float uus[SEG], dts[SEG], pres[SEG];
+    // state after step ts - 1 (zero at the start of the input)
+    const float* xc = xck + (int64_t)(ts / SEG - 1) * xck_step;
 #pragma unroll
-      for (int n = 0; n < NS; ++n) h[n] = s_seg[k][n][tid];
+    for (int n = 0; n < NS; ++n) hn[n] = (ts > 0 && n < N) ? xc[n] : 0.f;
+  };
+  const int nseg = (t1 - t0 + SEG - 1) / SEG;
+  fetch(t0 + (nseg - 1) * SEG);
+
+  // Scalar-cache pipeline over half rows (HS states) of B / C, as in the forward (touch /
+  // opaque, s6_common.h): consume the half row(s) in flight, issue the next, compute.
+  BCGroup<Tbc> bnx, cnx;
+  bnx.template load<HS>(Bbase + (uint32_t)((nseg - 1) * SEG) * Bst);
+
+  for (int s = nseg - 1; s >= 0; --s) {
+    const int ts = t0 + s * SEG;
+    const int te = min(ts + SEG, t1);
+    float uu[SEG], dt[SEG], dy[SEG], pre[SEG], hst[NS];
 #pragma unroll
-      for (int i = 0; i < SEG; ++i) {
-        const int64_t t = sg0 + i;
-        if (t < te) {
-          if (VARLEN && ((smask >> (uint32_t)(t - ts)) & 1u)) {
+    for (int i = 0; i < SEG; ++i) {
+      uu[i] = un[i];
+      pre[i] = dn[i] + bias;
+      dt[i] = prep_dt<DTM>(dn[i], bias);
+      dy[i] = on[i];
+      if (HAS_Z) {
+        // out_z = out * silu(z):  dy = dout silu(z),  dz = dout out sig (1 + z (1 - sig))
+        const float zz = zn[i], sg = sigmoidf_(zz);
+        dy[i] = on[i] * (zz * sg);
+        if (ts + i < te)
+          Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz,
+                          on[i] * yn[i] * sg * (1.f + zz * (1.f - sg)));
+      }
+    }
 #pragma unroll
-            for (int n = 0; n < NS; ++n) h[n] = 0.f;
+    for (int n = 0; n < NS; ++n) hst[n] = hn[n];
+    if (s > 0) fetch(ts - SEG);
+    const uint32_t smask = varlen ? start_mask(p.cu, p.nseq, ts, te) : 0u;
+    float s1[SEG], s2[SEG];
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) s1[i] = s2[i] = 0.f;
+
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) {
+      const uint32_t hoff = (uint32_t)(hh * HS * EB);
+      // Forward recompute of this half's states over the segment.
+      float hs[SEG][HS];
+      {
+        float h[HS];
+#pragma unroll
+        for (int k = 0; k < HS; ++k) h[k] = hst[hh * HS + k];
+#pragma unroll
+        for (int i = 0; i < SEG; ++i) {
+          if (ts + i < te) {
+            bnx.touch();
+            const BCGroup<Tbc> bcur = bnx;
+            if (ts + i + 1 < te) {
+              bnx.template load<HS>(Bbase + opaque((uint32_t)(ts + i + 1 - t0) * Bst + hoff));
+            } else {  // first step of the reverse sweep
+              bnx.template load<HS>(Bbase + opaque((uint32_t)(te - 1 - t0) * Bst + hoff));
+              cnx.template load<HS>(Cbase + opaque((uint32_t)(te - 1 - t0) * Cst + hoff));
+            }
+            const float dtu = dt[i] * uu[i];
+            auto body = [&](auto st_tag) {  // ST: a sequence starts at this step, h_{t-1} = 0
+              constexpr bool ST = decltype(st_tag)::value;
+#pragma unroll
+              for (int k = 0; k < HS; ++k) {
+                const float b_ = dtu * bcur.get(k);
+                h[k] = ST ? b_ : fmaf(fast_exp2(dt[i] * Ap[hh * HS + k]), h[k], b_);
+                hs[i][k] = h[k];
+              }
+            };
+            if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
           }
-          float Bv[NS];
-          BCLoad<Tbc>::template row<NS>(Bbase + t * Bstep, Bv);
-          const float uu = Elem<Tio>::load(p.u, ub + t * p.su[2]);
-          const float pre = Elem<Tio>::load(p.delta, db + t * p.sdl[2]) + bias;
-          const float dt = p.softplus ? softplus20(pre) : pre;
-          const float dtu = dt * uu;
-#pragma unroll
-          for (int n = 0; n < NS; ++n) {
-            h[n] = fmaf(fast_exp2(dt * Ap[n]), h[n], dtu * Bv[n]);
-            hs[i][n] = h[n];
-          }
-          uus[i] = uu;
-          dts[i] = dt;
-          pres[i] = pre;
         }
       }
+      // Reverse sweep.
 #pragma unroll
       for (int i = SEG - 1; i >= 0; --i) {
-        const int64_t t = sg0 + i;
+        const int t = ts + i;
         if (t < te) {
-          const bool st = VARLEN ? (((smask >> (uint32_t)(t - ts)) & 1u) != 0) : (t == 0);
-          float Bv[NS], Cv[NS];
-          BCLoad<Tbc>::template row<NS>(Bbase + t * Bstep, Bv);
-          BCLoad<Tbc>::template row<NS>(Cbase + t * Cstep, Cv);
-          const float uu = uus[i], dt = dts[i];
-          const float dtu = dt * uu;
-          const float dov = Elem<Tio>::load(p.dout, dob + t * p.sdo[2]);
-          float dy = dov;
-          if (p.has_z) {
-            const float zz = Elem<Tio>::load(p.z, zb + t * p.sz[2]);
-            const float sg = sigmoidf_(zz);
-            dy = dov * (zz * sg);
-            const float yo = Elem<Tio>::load(p.out, oub + t * p.sout[2]);
-            if (active) Elem<Tio>::store(p.dz, dzb + t * p.sdz[2], dov * yo * sg * (1.f + zz * (1.f - sg)));
-          }
-          float hp[NS];
+          bnx.touch();
+          cnx.touch();
+          const BCGroup<Tbc> bcur = bnx, ccur = cnx;
           if (i > 0) {
-#pragma unroll
-            for (int n = 0; n < NS; ++n) hp[n] = hs[i - 1][n];
-          } else {
-#pragma unroll
-            for (int n = 0; n < NS; ++n) hp[n] = s_seg[k][n][tid];
+            bnx.template load<HS>(Bbase + opaque((uint32_t)(t - 1 - t0) * Bst + hoff));
+            cnx.template load<HS>(Cbase + opaque((uint32_t)(t - 1 - t0) * Cst + hoff));
+          } else if (hh + 1 < NH) {  // next half, same segment
+            bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - t0) * Bst + hoff + HS * EB));
+          } else if (s > 0) {  // first half of the previous segment
+            bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - SEG - t0) * Bst));
           }
-          float s1 = 0.f, s2 = 0.f;
-          float pB[NS], pC[NS];
+          // Delta passes through an empty asm so that exp(Delta A) is recomputed here rather
+          // than kept live from the recompute above (64 more VGPRs per lane).
+          float dti = dt[i];
+          asm volatile("" : "+v"(dti));
+          const float dtu = dti * uu[i];
+          float pB[HS], pC[HS];
+          auto body = [&](auto st_tag) {  // ST: a sequence starts at this step
+            constexpr bool ST = decltype(st_tag)::value;
 #pragma unroll
-          for (int n = 0; n < NS; ++n) {
-            const float a = fast_exp2(dt * Ap[n]);
-            const float lam = fmaf(Cv[n], dy, gs[n]);
-            const float q = st ? 0.f : lam * (a * hp[n]);
-            dAacc[n] = fmaf(q, dt, dAacc[n]);
-            s2 = fmaf(q, Ap[n], s2);
-            s1 = fmaf(lam, Bv[n], s1);
-            pB[n] = active ? lam * dtu : 0.f;
-            pC[n] = active ? dy * hs[i][n] : 0.f;
-            gs[n] = st ? 0.f : a * lam;
-          }
-          s2 *= 0.69314718055994531f;  // Ap = A * log2(e)
-          const float duv = fmaf(dt, s1, Dv * dy);
-          float ddv = fmaf(uu, s1, s2);
-          if (p.softplus) ddv *= softplus20_grad(pres[i]);
-          if (active) {
-            Elem<Tio>::store(p.du, dub + t * p.sdu[2], duv);
-            Elem<Tio>::store(p.ddelta, ddb + t * p.sddl[2], ddv);
-          }
-          dDacc = fmaf(dy, uu, dDacc);
-          dbacc += ddv;
-          wave_transpose_reduce16(pB, lane);
-          wave_transpose_reduce16(pC, lane);
-          if ((lane & 3) == 0) {
-            s_red[0][i][wv][lane >> 2] = pB[0];
-            s_red[1][i][wv][lane >> 2] = pC[0];
+            for (int k = 0; k < HS; ++k) {
+              const int n = hh * HS + k;
+              const float lam = fmaf(ccur.get(k), dy[i], gs[n]);
+              if (!ST) {
+                const float a = fast_exp2(dti * Ap[n]);
+                const float hp = (i > 0) ? hs[i - 1][k] : hst[n];
+                const float q = lam * (a * hp);
+                dAacc[n] = fmaf(q, dti, dAacc[n]);
+                s2[i] = fmaf(q, Ap[n], s2[i]);
+                gs[n] = a * lam;
+              } else {
+                gs[n] = 0.f;
+              }
+              s1[i] = fmaf(lam, bcur.get(k), s1[i]);
+              pB[k] = lam * dtu;
+              pC[k] = dy[i] * hs[i][k];
+            }
+          };
+          if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
+          wave_transpose_reduce8(pB, lane);
+          wave_transpose_reduce8(pC, lane);
+          const int nn = hh * HS + ((lane >> 3) & 7);
+          if ((lane & 7) == 0 && nn < N) {
+            pBrow[(int64_t)t * kPartRow + nn] = pB[0];
+            pCrow[(int64_t)t * kPartRow + nn] = pC[0];
           }
         }
       }
-      __syncthreads();
-      {
-        const int which = tid >> 7;
-        const int i = (tid >> 4) & 7;
-        const int n = tid & 15;
-        const int64_t t = sg0 + i;
-        if (t < te && n < N) {
-          const float v = s_red[which][i][0][n] + s_red[which][i][1][n] + s_red[which][i][2][n] +
-                          s_red[which][i][3][n];
-          (which ? pCrow : pBrow)[t * p.N + n] = v;
-        }
+    }
+    // Per-step outputs of the segment.
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) {
+      if (ts + i < te) {
+        const uint32_t r = (uint32_t)(ts + i - t0);
+        const float duv = fmaf(dt[i], s1[i], Dv * dy[i]);
+        float ddv = fmaf(uu[i], s1[i], s2[i] * 0.69314718055994531f);  // Ap = A log2(e)
+        if (DTM == kDtSoftplus) ddv *= softplus20_grad(pre[i]);
+        Buf<Tio>::store(rs_du, vo_du, r * st_du, duv);
+        Buf<Tio>::store(rs_dd, vo_dd, r * st_dd, ddv);
+        dDacc = fmaf(dy[i], uu[i], dDacc);
+        dbacc += ddv;
       }
-      __syncthreads();
     }
   }
   if (active) {
+    const int64_t row = b * p.K + c;
+    float* dAp = p.ws_dA + (row * p.D + d) * p.N;
 #pragma unroll
     for (int n = 0; n < NS; ++n)
-      if (n < N) atomicAdd(p.dA + d * p.sdA[0] + n * p.sdA[1], dAacc[n]);
-    if (p.has_D) atomicAdd(p.dD + d * p.sdD, dDacc);
-    if (p.has_bias) atomicAdd(p.dbias + d * p.sdbias, dbacc);
+      if (n < N) dAp[n] = dAacc[n];
+    if (p.has_D) p.ws_dD[row * p.D + d] = dDacc;
+    if (p.has_bias) p.ws_db[row * p.D + d] = dbacc;
   }
 }
 
-// dB[b, g, n, t] = sum over 256-channel blocks of the partials.
-__global__ void __launch_bounds__(256) bwd_reduce_bc(BwdK p) {
-  const int64_t total = p.Bsz * p.G * p.L * p.N;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = i % p.N;
-    int64_t r = i / p.N;
-    const int64_t t = r % p.L;
-    r /= p.L;
-    const int64_t g = r % p.G;
-    const int64_t b = r / p.G;
-    const int64_t base = (b * p.G + g) * p.nJ4;
-    float sb = 0.f, sc = 0.f;
-    for (int64_t j = 0; j < p.nJ4; ++j) {
-      sb += p.ws_pB[((base + j) * p.L + t) * p.N + n];
-      sc += p.ws_pC[((base + j) * p.L + t) * p.N + n];
-    }
-    p.dB[b * p.sdB[0] + g * p.sdB[1] + n * p.sdB[2] + t * p.sdB[3]] = sb;
-    p.dC[b * p.sdC[0] + g * p.sdC[1] + n * p.sdC[2] + t * p.sdC[3]] = sc;
-  }
-}
+// ---------------------------------------------------------------------------------------
 
-static hipError_t record(void* const* ev, int i, hipStream_t st) {
-  if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
-  return hipEventRecord((hipEvent_t)ev[i], st);
-}
-
-template <typename Tio, typename Tbc, bool VARLEN>
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
 static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st, void* const* ev) {
   hipError_t e;
+  const int64_t nx = k.Bsz * k.nDblk;
   if (k.K > 1) {
-    dim3 grid((unsigned)(k.Bsz * k.nDblk), (unsigned)(k.K - 1));
-    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, 16, VARLEN>), grid, dim3(kWave), 0, st, k);
+    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, k.K - 1), dim3(kWave),
+                       0, st, k);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const int64_t total = k.Bsz * k.D * k.N;
-    hipLaunchKernelGGL(bwd_carry, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, k);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_bwd_carry(k, st)) != hipSuccess) return e;
   }
-  dim3 grid((unsigned)(k.Bsz * k.G * k.nJ4), (unsigned)k.K);
-  if ((e = record(ev, 0, st)) != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_main<Tio, Tbc, VARLEN>), grid, dim3(256), 0, st, k);
+  if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
+  hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, k.K), dim3(kWave), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if ((e = record(ev, 1, st)) != hipSuccess) return e;
-  const int64_t total = k.Bsz * k.G * k.L * k.N;
-  int64_t blocks = (total + 255) / 256;
-  if (blocks > 65535) blocks = 65535;
-  hipLaunchKernelGGL(bwd_reduce_bc, dim3((unsigned)blocks), dim3(256), 0, st, k);
-  return hipGetLastError();
+  if ((e = record_event(ev, 1, st)) != hipSuccess) return e;
+  return launch_bwd_reduce(k, st);
+}
+
+template <typename Tio, typename Tbc, int NS, int DTM>
+static hipError_t launch_bwd_z(const BwdK& k, hipStream_t st, void* const* ev) {
+  return k.has_z ? launch_bwd_t<Tio, Tbc, NS, DTM, true>(k, st, ev)
+                 : launch_bwd_t<Tio, Tbc, NS, DTM, false>(k, st, ev);
+}
+
+template <typename Tio, typename Tbc, int NS>
+static hipError_t launch_bwd_dt(const BwdK& k, hipStream_t st, void* const* ev) {
+  switch (dt_mode(k.has_bias, k.softplus)) {
+    case kDtRaw: return launch_bwd_z<Tio, Tbc, NS, kDtRaw>(k, st, ev);
+    case kDtBias: return launch_bwd_z<Tio, Tbc, NS, kDtBias>(k, st, ev);
+    default: return launch_bwd_z<Tio, Tbc, NS, kDtSoftplus>(k, st, ev);
+  }
 }
 
 template <typename Tio, typename Tbc>
-static hipError_t launch_bwd_v(const BwdK& k, hipStream_t st, void* const* ev) {
-  return k.nseq > 0 ? launch_bwd_t<Tio, Tbc, true>(k, st, ev)
-                    : launch_bwd_t<Tio, Tbc, false>(k, st, ev);
+static hipError_t launch_bwd_bc(const BwdK& k, hipStream_t st, void* const* ev) {
+  return k.N <= 8 ? launch_bwd_dt<Tio, Tbc, 8>(k, st, ev) : launch_bwd_dt<Tio, Tbc, 16>(k, st, ev);
 }
 
 template <typename Tio>
-static hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
-  switch (bc_dtype) {
-    case S6_F32: return launch_bwd_v<Tio, float>(k, st, ev);
-    case S6_BF16: return launch_bwd_v<Tio, bf16>(k, st, ev);
-    default: return launch_bwd_v<Tio, f16>(k, st, ev);
-  }
+hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (bc_dtype == S6_F32) return launch_bwd_bc<Tio, float>(k, st, ev);
+  return launch_bwd_bc<Tio, Tio>(k, st, ev);
 }
 
-hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev) {
-  switch (io_dtype) {
-    case S6_F32: return launch_bwd_io<float>(k, bc_dtype, st, ev);
-    case S6_BF16: return launch_bwd_io<bf16>(k, bc_dtype, st, ev);
-    default: return launch_bwd_io<f16>(k, bc_dtype, st, ev);
-  }
-}
+template hipError_t launch_bwd_io<S6_TIO>(const BwdK&, int, hipStream_t, void* const*);
 
 }  // namespace s6

@@ -94,12 +94,18 @@ template <> struct Buf<f16> {
 // 16-bit formats are loaded as packed 32-bit pairs and unpacked on the scalar unit.
 typedef const __attribute__((address_space(4))) uint32_t* cu32p;
 
+// An empty asm that reads 8 SGPR words: the compiler must complete their loads before it.
+__device__ inline void touch_words(const uint32_t (&w)[8]) {
+  asm volatile("" ::"s"(w[0]), "s"(w[1]), "s"(w[2]), "s"(w[3]), "s"(w[4]), "s"(w[5]), "s"(w[6]),
+               "s"(w[7]));
+}
+
 // A group of up to 16 consecutive states of one B or C row, as raw 32-bit words in SGPRs.
 // The 16-bit formats stay packed two per word until the value is used.
 template <typename T> struct BCGroup;
 template <> struct BCGroup<float> {
-  static constexpr int kWords = 16;
-  uint32_t w[16];
+  static constexpr int kWords = 8;
+  uint32_t w[8];
   template <int G>
   __device__ inline void load(const char* row) {
     cu32p r = (cu32p)row;
@@ -107,6 +113,7 @@ template <> struct BCGroup<float> {
     for (int i = 0; i < G; ++i) w[i] = r[i];
   }
   __device__ inline float get(int n) const { return __uint_as_float(w[n]); }
+  __device__ inline void touch() const { touch_words(w); }
 };
 template <> struct BCGroup<bf16> {
   static constexpr int kWords = 8;
@@ -121,6 +128,7 @@ template <> struct BCGroup<bf16> {
     const uint32_t x = w[n >> 1];
     return (n & 1) ? __uint_as_float(x & 0xffff0000u) : __uint_as_float(x << 16);
   }
+  __device__ inline void touch() const { touch_words(w); }
 };
 template <> struct BCGroup<f16> {
   static constexpr int kWords = 8;
@@ -135,6 +143,7 @@ template <> struct BCGroup<f16> {
     const uint32_t x = w[n >> 1];
     return (float)__builtin_bit_cast(_Float16, (uint16_t)((n & 1) ? (x >> 16) : (x & 0xffffu)));
   }
+  __device__ inline void touch() const { touch_words(w); }
 };
 
 // Whole-row loads (NS values) for the backward kernels.
@@ -153,6 +162,9 @@ template <typename T> struct BCLoad {
   }
 };
 
+// States of one B/C row that one scalar group (8 words, s_load_dwordx8) holds.
+template <typename T> constexpr int kGroupStates = 32 / Elem<T>::kSize;
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // F.softplus with beta=1, threshold=20 (selective_scan_interface.py:111-112).
@@ -165,6 +177,48 @@ __device__ inline float softplus20_grad(float x) {
 }
 __device__ inline float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
+// How Delta is formed from the delta input (selective_scan_interface.py:107-112): as is,
+// plus delta_bias, or softplus(delta + delta_bias) (bias 0 when absent).
+enum DtMode { kDtRaw = 0, kDtBias = 1, kDtSoftplus = 2 };
+inline int dt_mode(int has_bias, int softplus) {
+  return softplus ? kDtSoftplus : (has_bias ? kDtBias : kDtRaw);
+}
+template <int DTM>
+__device__ inline float prep_dt(float raw, float bias) {
+  if constexpr (DTM == kDtRaw) return raw;
+  else if constexpr (DTM == kDtBias) return raw + bias;
+  else return softplus20(raw + bias);
+}
+
+// Scalar-load pipelining.  Scalar loads complete out of order, so the compiler can only
+// wait for all of them (lgkmcnt(0)); and loads from the constant address space are
+// invariant, so LLVM may hoist the next row's load above the point where the current row
+// is first consumed -- which makes every wait cover a load that was just issued.  The
+// pattern used by the scans is therefore
+//     cur.touch();                 // consume the group in flight: the compiler waits here
+//     off = opaque(off);           // the next address is only known after that point
+//     nxt.load(base + off);        // ... so the next load is issued after the wait
+// which leaves one group of compute between a load and its wait.
+__device__ inline uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X, each with its own
+// L2.  The kernels take a 1-D grid and remap the linear id so that consecutive logical
+// blocks -- the channel blocks of one (batch, chunk), which read the same B/C rows --
+// run on the same XCD.  Logical block = (x, y) with x fastest, x < nx.
+struct BlockPos {
+  int64_t x, y;
+};
+__device__ inline BlockPos block_pos(int64_t nx) {
+  const int64_t total = gridDim.x;
+  int64_t id = blockIdx.x;
+  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  return {id % nx, id / nx};
+}
+inline dim3 xcd_grid(int64_t nx, int64_t ny) { return dim3((unsigned)(nx * ny)); }
+
 // Kernel parameter block shared by the forward kernels (plain values; strides in elements).
 struct FwdK {
   int64_t Bsz, D, L, N, G;
@@ -176,14 +230,14 @@ struct FwdK {
   const void* Bm; const void* Cm;
   const int32_t* cu; int32_t nseq;
   void* out; void* out_z;
-  float* x_ckpt; int64_t nck;
+  float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N]
   float* last_state;
   float* ws_h;    // [Bsz*D, K, N]  chunk summaries, then carried-in states
-  float* ws_s;    // [Bsz*D, K]     sum of Delta since the last reset in the chunk
-  int32_t* ws_r;  // [K]            1 if a sequence starts inside the chunk
+  float* ws_s;    // [Bsz*D, K]     sum of Delta since the last sequence start in the chunk
+  int32_t* ws_r;  // [Bsz*D, K]     1 if a sequence starts inside the chunk (varlen only)
   int64_t K, Lc;  // number of chunks and chunk length (multiple of kCk)
   int32_t has_D, has_z, has_bias, softplus;
-  int64_t nDblk;  // ceil(D / 64)
+  int64_t nDblk;  // G * ceil(D / G / 64): 64-channel blocks per batch
 };
 
 }  // namespace s6

@@ -1,8 +1,53 @@
-// Internal launch interface between the C ABI (s6_abi.cpp) and the HIP kernels.
+// Internal launch interface between the C ABI (s6_abi.cpp) and the HIP kernels, and the
+// device helpers the kernel files share.
 #pragma once
 #include "s6_common.h"
 
 namespace s6 {
+
+// Sequence bookkeeping for packed varlen input: index into cu_seqlens of the first
+// sequence start >= t0, and that start (INT64_MAX past the last one).
+struct SeqCursor {
+  int32_t idx;
+  int64_t pending;
+};
+
+__device__ inline SeqCursor seq_cursor_at(const int32_t* cu, int32_t nseq, int64_t t0) {
+  int32_t lo = 0, hi = nseq + 1;  // first i with cu[i] >= t0 (cu non-decreasing)
+  while (lo < hi) {
+    int32_t mid = (lo + hi) >> 1;
+    if ((int64_t)cu[mid] < t0) lo = mid + 1; else hi = mid;
+  }
+  SeqCursor s;
+  s.idx = lo;
+  s.pending = (lo <= nseq) ? (int64_t)cu[lo] : INT64_MAX;
+  return s;
+}
+
+// True when a sequence starts at some step of [t0, t1).
+__device__ inline bool range_has_start(const int32_t* cu, int32_t nseq, int64_t t0, int64_t t1) {
+  return seq_cursor_at(cu, nseq, t0).pending < t1;
+}
+
+// Bit i set when a sequence starts at step ts + i, for i in [0, te - ts), te - ts <= 32.
+__device__ inline uint32_t start_mask(const int32_t* cu, int32_t nseq, int64_t ts, int64_t te) {
+  SeqCursor s = seq_cursor_at(cu, nseq, ts);
+  uint32_t m = 0;
+  for (int32_t i = s.idx; i <= nseq && (int64_t)cu[i] < te; ++i) m |= 1u << (uint32_t)(cu[i] - ts);
+  return m;
+}
+
+// Stores the first N (<= NS) states of one lane to a contiguous fp32 row.
+template <int NS>
+__device__ inline void store_state(float* dst, const float (&h)[NS], int N) {
+  if (N == NS && (NS % 4) == 0) {
+#pragma unroll
+    for (int n = 0; n < NS; n += 4)
+      *reinterpret_cast<float4*>(dst + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+  } else {
+    for (int n = 0; n < N; ++n) dst[n] = h[n];
+  }
+}
 
 // Parameter block of the backward kernels (strides in elements).
 struct BwdK {
@@ -10,24 +55,56 @@ struct BwdK {
   int64_t su[3], sdl[3], sz[3], sdo[3], sout[3], sdu[3], sddl[3], sdz[3];
   int64_t sA[2], sD, sbias;
   int64_t sB[4], sC[4];
-  int64_t sdA[2], sdD, sdbias;
   int64_t sdB[4], sdC[4];
   const void* u; const void* delta; const void* z; const void* dout; const void* out;
   const float* A; const float* Dp; const float* bias;
   const void* Bm; const void* Cm;
   const int32_t* cu; int32_t nseq;
-  const float* x_ckpt; int64_t nck;
+  const float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N], as written by the forward
   void* du; void* ddelta; void* dz;
   float* dA; float* dD; float* dbias; float* dB; float* dC;
-  float* ws_g;   // [Bsz*D, K, N]  reverse chunk summaries, then carried-in gradients
-  float* ws_s;   // [Bsz*D, K]     sum of Delta over each chunk
-  float* ws_pB;  // [Bsz, G, nJ4, L, N]  per-channel-block partial dB
-  float* ws_pC;  // [Bsz, G, nJ4, L, N]  per-channel-block partial dC
+  int64_t sdA[2], sdD, sdbias;
+  float* ws_g;   // [Bsz*D, K, N]     reverse chunk summaries, then carried-in gradients
+  float* ws_s;   // [Bsz*D, K]        sum of Delta over each chunk
+  int32_t* ws_r; // [Bsz*D, K]        1 if a sequence starts inside the chunk (varlen only)
+  float* ws_pB;  // [Bsz, G, nJ, L, kPartRow]  per-64-channel-block partial dB
+  float* ws_pC;  // [Bsz, G, nJ, L, kPartRow]  per-64-channel-block partial dC
+  float* ws_dA;  // [Bsz*K, D, N]     per-(batch, chunk) partial dA
+  float* ws_dD;  // [Bsz*K, D]        per-(batch, chunk) partial dD
+  float* ws_db;  // [Bsz*K, D]        per-(batch, chunk) partial ddelta_bias
   int64_t K, Lc;
-  int64_t nDblk;   // G * ceil(Dg / 64)   (summary kernel, 64-channel blocks)
-  int64_t nJ4;     // ceil(Dg / 256)      (main kernel, 256-channel blocks per group)
+  int64_t nDblk;   // G * nJ: 64-channel blocks per batch
+  int64_t nJ;      // ceil(Dg / 64)
   int32_t has_D, has_z, has_bias, softplus;
 };
+
+// Row width of the backward's partial dB / dC buffers (dstate <= 16, zero-padded rows).
+constexpr int kPartRow = 16;
+
+// Parameter block of the inter-chunk carry kernels.
+struct CarryK {
+  const float* A; int64_t sA[2];
+  float* ws;             // [nch, K, N] summaries in, carried values out
+  const float* ws_s;     // [nch, K] sum of Delta per chunk
+  const int32_t* ws_r;   // [nch, K] 1 when a sequence starts inside the chunk; NULL: none do
+  int64_t nch, D, K, N;
+};
+
+inline hipError_t record_event(void* const* ev, int i, hipStream_t st) {
+  if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
+  return hipEventRecord((hipEvent_t)ev[i], st);
+}
+
+// Per input dtype (one translation unit each): the dtype-templated scan kernels.
+template <typename Tio>
+hipError_t launch_fwd_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
+template <typename Tio>
+hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
+
+// s6_misc.hip: carries, reductions, fills, B/C relayout.
+hipError_t launch_fwd_carry(const FwdK& k, hipStream_t st);
+hipError_t launch_bwd_carry(const BwdK& k, hipStream_t st);
+hipError_t launch_bwd_reduce(const BwdK& k, hipStream_t st);
 
 // ev (nullable): hipEvent_t pair recorded around the main scan kernel.
 hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev);

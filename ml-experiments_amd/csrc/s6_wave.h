@@ -34,39 +34,40 @@ __device__ inline float dpp_quad_xor2(float v) {
                                                                0x4E, 0xf, 0xf, false));
 }
 
-// Sum v[n] over the 64 lanes of the wave for n = 0..15.  On return every lane l holds in
-// v[0] the sum for n = l / 4 (each group of 4 lanes holds the same value).
-__device__ inline void wave_transpose_reduce16(float (&v)[16], int lane) {
-  // lanes l and l^32: swap halves of (v[i], v[i+8]) -> low half keeps n=i, high n=i+8
+// Sum v[n] over the 64 lanes of the wave for n = 0..7.  On return v[0] on lane l holds the
+// sum for n = (l >> 3) & 7 (each group of 8 consecutive lanes holds the same value).
+// 4 + 2 permlane swaps, 2 selects and 7 adds for 8 sums.
+__device__ inline void wave_transpose_reduce8(float (&v)[8], int lane) {
+  // lanes l and l^32: the low half keeps n = i, the high half n = i + 4
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %4\n\t"
+      "v_permlane32_swap_b32 %1, %5\n\t"
+      "v_permlane32_swap_b32 %2, %6\n\t"
+      "v_permlane32_swap_b32 %3, %7\n\t"
+      "s_nop 1"
+      : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
+        "+v"(v[7]));
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    permlane32_swap(v[i], v[i + 8]);
-    v[i] = v[i] + v[i + 8];
-  }
-  // lanes l and l^16: row r keeps n = 4r + i for i < 4
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    permlane16_swap(v[i], v[i + 4]);
-    v[i] = v[i] + v[i + 4];
-  }
-  // lanes l and l^8 inside a row: the low 8 lanes keep i, the high 8 keep i + 2
+  for (int i = 0; i < 4; ++i) v[i] += v[i + 4];
+  // lanes l and l^16: row r keeps n = i + 2 (r & 1) + 4 (r >> 1) for i < 2
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %2\n\t"
+      "v_permlane16_swap_b32 %1, %3\n\t"
+      "s_nop 1"
+      : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+  v[0] += v[2];
+  v[1] += v[3];
+  // lanes l and l^8 inside a row: the low 8 lanes keep i = 0, the high 8 keep i = 1
   const bool hi8 = (lane & 8) != 0;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float send = hi8 ? v[i] : v[i + 2];
-    float keep = hi8 ? v[i + 2] : v[i];
-    v[i] = keep + dpp_row_ror8(send);
-  }
-  // lanes l and 7-l inside each 8-lane half: the low 4 keep v[0], the high 4 keep v[1]
-  {
-    const bool hi4 = (lane & 4) != 0;
-    float send = hi4 ? v[0] : v[1];
-    float keep = hi4 ? v[1] : v[0];
-    v[0] = keep + dpp_row_half_mirror(send);
-  }
+  const float send = hi8 ? v[0] : v[1];
+  const float keep = hi8 ? v[1] : v[0];
+  v[0] = keep + dpp_row_ror8(send);
+  // sum over the 8 lanes of each half-row (bits 0-2 of the lane)
   v[0] += dpp_quad_xor1(v[0]);
   v[0] += dpp_quad_xor2(v[0]);
+  v[0] += dpp_row_half_mirror(v[0]);
 }
-
 
 }  // namespace s6

@@ -14,8 +14,8 @@ import os
 
 import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 
-ABI_VERSION = 1
-CKPT_INTERVAL = 32
+ABI_VERSION = 2
+CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 16
 

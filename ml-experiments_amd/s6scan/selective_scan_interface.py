@@ -143,7 +143,7 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         out = torch.empty_like(u)
         out_z = torch.empty_like(u) if z is not None else None
         nck = _lib.LIB.s6_num_checkpoints(ctypes.byref(prob))
-        x_ckpt = (torch.empty(batch, dim, nck, dstate, dtype=torch.float32, device=u.device)
+        x_ckpt = (torch.empty(batch, nck, dim, dstate, dtype=torch.float32, device=u.device)
                   if want_ckpt else None)
         nls = nseq if nseq > 0 else batch
         last_state = (torch.empty(nls, dim, dstate, dtype=torch.float32, device=u.device)

@@ -68,7 +68,8 @@ def test_invalid_problems(kw, code, msg):
 
 
 def test_num_checkpoints():
-    for L, want in ((1, 1), (32, 1), (33, 2), (4096, 128)):
+    # one entry per S6_CKPT_INTERVAL (8) steps, the last one possibly partial
+    for L, want in ((1, 1), (8, 1), (9, 2), (32, 4), (33, 5), (4096, 512)):
         assert _lib.LIB.s6_num_checkpoints(ctypes.byref(prob(seqlen=L))) == want
 
 
