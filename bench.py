@@ -45,7 +45,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="fwd1", choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4"])
+    ap.add_argument("--workload", default="fwd1",
+                    choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -89,6 +90,20 @@ def cpu_baseline(cfg, make_inputs):
     }
 
 
+def copy_reference(torch, steps):
+    """Plain device-to-device copy of a known size (1 GiB read + 1 GiB written per launch).
+    Profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between those
+    counters and true HBM bytes that the scan kernels' counter readings are scaled by."""
+    n = 1 << 28  # fp32 elements = 1 GiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(max(steps, 1)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "copyref", "bytes_read_per_launch": 4 * n,
+                      "bytes_written_per_launch": 4 * n, "launches": max(steps, 1)}))
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -99,6 +114,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.workload == "copyref":
+        copy_reference(torch, args.steps)
+        return
     import s6scan
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
@@ -165,14 +183,20 @@ def main():
     # Dominant kernel: the scan/output pass of the forward (backward main kernel for the
     # fwd+bwd workloads); one launch processes every (token, channel) of the call.
     if cfg.backward:
-        dom_name, dom_ms, dom_bytes = "bwd_main", kb_ms, nbytes - fwd_bytes
+        dom_name, dom_ms, dom_bytes = "bwd_scan", kb_ms, nbytes - fwd_bytes
     else:
         dom_name, dom_ms, dom_bytes = "fwd_scan (output pass)", k_ms, fwd_bytes
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    traffic = None
+    # HBM bytes per launch of the dominant kernel and its VALU busy fraction, measured with
+    # rocprofv3 (FETCH_SIZE / WRITE_SIZE scaled by a plain-copy calibration; SQ counters) and
+    # committed under profiles/.
+    traffic = valu_busy = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get(args.workload)
+            prof = json.load(f).get(args.workload)
+        if prof:
+            traffic = round(prof["traffic_bytes_per_launch"])
+            valu_busy = round(prof["kernels"][prof["dominant_kernel"]]["valu_busy"], 3)
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -203,6 +227,9 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 5),
             "traffic": traffic,
             "kernel_ms": round(dom_ms, 5),
+            # The kernels are VALU-bound (exp + 4-5 FMA-class ops per state element, packed
+            # FP32 disabled); this is the measured fraction of SIMD cycles issuing VALU work.
+            "valu_busy": valu_busy,
         },
     }
     if cfg.backward:

@@ -27,8 +27,13 @@ int ok() {
   return S6_OK;
 }
 
-constexpr int64_t kTargetWaves = 4096;  // 16 waves per CU on a 256-CU MI355X
-constexpr int64_t kMinChunk = 128;
+// Chunking targets (waves per launch; shortest chunk).  The forward scan holds ~90 VGPRs
+// (5 waves per SIMD) and is VALU-bound at 4 waves per SIMD; the backward scan holds ~240
+// VGPRs (2 waves per SIMD) and needs more waves in flight to cover its memory latency.
+constexpr int64_t kTargetWavesFwd = 4096;  // 4 per SIMD on a 256-CU MI355X
+constexpr int64_t kTargetWavesBwd = 8192;
+constexpr int64_t kMinChunkFwd = 128;
+constexpr int64_t kMinChunkBwd = 128;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -66,9 +71,10 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   pl.nJ = ceil_div(pl.Dg, 64);
   pl.nDblk = p.ngroups * pl.nJ;
   const int64_t chw = p.batch * pl.nDblk;
-  const int64_t ktarget = ceil_div(kTargetWaves, chw > 0 ? chw : 1);
+  const int64_t ktarget = ceil_div(bwd ? kTargetWavesBwd : kTargetWavesFwd, chw > 0 ? chw : 1);
   int64_t Lc = ceil_div(p.seqlen, ktarget > 0 ? ktarget : 1);
-  if (Lc < kMinChunk) Lc = kMinChunk;
+  const int64_t min_chunk = bwd ? kMinChunkBwd : kMinChunkFwd;
+  if (Lc < min_chunk) Lc = min_chunk;
   Lc = ceil_div(Lc, s6::kCk) * s6::kCk;
   pl.Lc = Lc;
   pl.K = ceil_div(p.seqlen, Lc);

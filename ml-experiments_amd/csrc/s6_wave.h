@@ -17,21 +17,23 @@ __device__ inline void permlane16_swap(float& a, float& b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
 
+// DPP lane permutations within 16-lane rows.  Each one is a full permutation (every lane
+// reads a valid source), so bound_ctrl is set and the move can fold into the consuming add.
 __device__ inline float dpp_row_ror8(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x128, 0xf, 0xf, false));
+                                                               0x128, 0xf, 0xf, true));
 }
 __device__ inline float dpp_row_half_mirror(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x141, 0xf, 0xf, false));
+                                                               0x141, 0xf, 0xf, true));
 }
 __device__ inline float dpp_quad_xor1(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0xB1, 0xf, 0xf, false));
+                                                               0xB1, 0xf, 0xf, true));
 }
 __device__ inline float dpp_quad_xor2(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x4E, 0xf, 0xf, false));
+                                                               0x4E, 0xf, 0xf, true));
 }
 
 // Sum v[n] over the 64 lanes of the wave for n = 0..7.  On return v[0] on lane l holds the
