@@ -52,7 +52,7 @@ extern "C" {
 #define S6_ABI_VERSION 2
 #define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
-#define S6_MAX_DSTATE_BWD 16
+#define S6_MAX_DSTATE_BWD 64
 
 enum s6_dtype { S6_F32 = 0, S6_BF16 = 1, S6_F16 = 2 };
 

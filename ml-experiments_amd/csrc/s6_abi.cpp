@@ -45,14 +45,16 @@ struct Plan {
   bool relayout_B, relayout_C;
   int64_t NP;  // padded dstate of relaid-out B / C
   size_t off_h, off_s, off_r, off_B, off_C, total_fwd;
-  size_t off_pB, off_pC, off_dA, off_dD, off_db, total_bwd;
+  size_t off_pB, off_pC, off_dA, off_dD, off_db, off_s12, total_bwd;
+  int64_t nsg, NPr;  // backward: state groups of 16, partial row width
 };
 
-// States held per lane by the kernels: the forward pads dstate to 8/16/32/64, the backward
-// to 8/16.  B and C rows are read as NS contiguous values, so a row is used in place only
-// when dstate == NS, the state axis is contiguous and 16-bit rows are 4-byte aligned.
+// States held per lane by the kernels: the forward pads dstate to 8/16/32/64; the backward
+// to 8/16 and, above 16, splits it into groups of 16 (padded to a multiple of 16).  B and C
+// rows are read as NS contiguous values, so a row is used in place only when dstate == NS,
+// the state axis is contiguous and 16-bit rows are 4-byte aligned.
 int64_t ns_fwd(int64_t N) { return N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
-int64_t ns_bwd(int64_t N) { return N <= 8 ? 8 : 16; }
+int64_t ns_bwd(int64_t N) { return N <= 8 ? 8 : ceil_div(N, s6::kBwdGroup) * s6::kBwdGroup; }
 
 bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_t NS) {
   if (N != NS || s[2] != 1) return false;
@@ -97,7 +99,9 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   pl.off_C = off;
   off += pl.relayout_C ? bc_bytes : 0;
   pl.total_fwd = off;
-  const size_t part = align256((size_t)(p.batch * p.ngroups * pl.nJ * p.seqlen * s6::kPartRow) * 4);
+  pl.nsg = p.dstate <= s6::kBwdGroup ? 1 : ceil_div(p.dstate, s6::kBwdGroup);
+  pl.NPr = pl.nsg * s6::kBwdGroup;
+  const size_t part = align256((size_t)(p.batch * p.ngroups * pl.nJ * p.seqlen * pl.NPr) * 4);
   pl.off_pB = off;
   off += part;
   pl.off_pC = off;
@@ -109,6 +113,9 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   off += p.has_D ? align256(rows * p.dim * 4) : 0;
   pl.off_db = off;
   off += p.has_delta_bias ? align256(rows * p.dim * 4) : 0;
+  pl.off_s12 = off;  // two [nsg, batch, seqlen, dim] fp32 buffers when dstate > 16
+  const size_t s12 = pl.nsg > 1 ? align256((size_t)(pl.nsg * p.batch * p.seqlen * p.dim) * 4) : 0;
+  off += 2 * s12;
   pl.total_bwd = off;
   return pl;
 }
@@ -390,8 +397,11 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.ws_dA = (float*)(ws + pl.off_dA);
     k.ws_dD = p.has_D ? (float*)(ws + pl.off_dD) : nullptr;
     k.ws_db = p.has_delta_bias ? (float*)(ws + pl.off_db) : nullptr;
+    const size_t s12 = pl.nsg > 1 ? align256((size_t)(pl.nsg * p.batch * p.seqlen * p.dim) * 4) : 0;
+    k.ws_s1 = pl.nsg > 1 ? (float*)(ws + pl.off_s12) : nullptr;
+    k.ws_s2 = pl.nsg > 1 ? (float*)(ws + pl.off_s12 + s12) : nullptr;
     k.K = pl.K; k.Lc = pl.Lc;
-    k.nDblk = pl.nDblk; k.nJ = pl.nJ;
+    k.nDblk = pl.nDblk; k.nJ = pl.nJ; k.nsg = pl.nsg; k.NPr = pl.NPr;
     k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
     e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st, a->kernel_events);
   }

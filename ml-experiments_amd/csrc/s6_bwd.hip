@@ -19,6 +19,7 @@
 //                dstate 16) so the segment's states fit in VGPRs.  dB / dC are reduced over the
 //                64 lanes with permlane swaps and DPP and written as one partial per wave;
 //                dA / dD / ddelta_bias as one partial per (batch, chunk).
+//   bwd_finish   (dstate > 16 only) du / ddelta from the per-state-group sums.
 //   bwd_reduce_* fixed-order sums of the partials (s6_misc.hip): the result is deterministic.
 #include <type_traits>
 
@@ -45,16 +46,17 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   const bool active = dloc < Dg;
   const int64_t d0 = g * Dg + j * kWave;
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int c = (int)bp.y + 1;
+  const int c = 1 + (int)(bp.y % (p.K - 1));
+  const int s0 = (int)(bp.y / (p.K - 1)) * NS;  // first state of this wave's state group
   const int t0 = c * (int)p.Lc;
   const int t1 = min(t0 + (int)p.Lc, (int)p.L);
-  const int N = (int)p.N;
+  const int N = (int)p.N - s0;                   // states of the group (may exceed NS)
   const bool varlen = p.nseq > 0;
 
   float Ap[NS], gs[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    Ap[n] = (n < N) ? p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e : 0.f;
+    Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
     gs[n] = 0.f;
   }
   const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
@@ -67,7 +69,8 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   const uint32_t vo_z = (HAS_Z && active) ? (uint32_t)(lane * p.sz[1] * ES) : kOffDrop;
   const uint32_t st_o = (uint32_t)(p.sdo[2] * ES), st_d = (uint32_t)(p.sdl[2] * ES);
   const uint32_t st_z = HAS_Z ? (uint32_t)(p.sz[2] * ES) : 0u;
-  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const char* const Cbase =
+      (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3] + s0) * EB;
   const uint32_t Cst = (uint32_t)(p.sC[3] * EB);
 
   float on[TB], dn[TB], zn[TB];
@@ -132,16 +135,21 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   }
   if (active) {
     const int64_t ch = b * p.D + d;
-    float* go = p.ws_g + (ch * p.K + c) * p.N;
+    float* go = p.ws_g + (ch * p.K + c) * p.N + s0;
 #pragma unroll
     for (int n = 0; n < NS; ++n)
       if (n < N) go[n] = gs[n];
-    p.ws_s[ch * p.K + c] = ssum;
-    if (varlen) p.ws_r[ch * p.K + c] = seen_start ? 1 : 0;
+    if (s0 == 0) {
+      p.ws_s[ch * p.K + c] = ssum;
+      if (varlen) p.ws_r[ch * p.K + c] = seen_start ? 1 : 0;
+    }
   }
 }
 
-template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+// MULTI: dstate > 16.  Each wave handles one group of NS (16) states; the per-step sums
+// over states that du / dDelta need are written per group (ws_s1 / ws_s2) and combined by
+// bwd_finish.
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI>
 __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_scan(BwdK p) {
   constexpr int SEG = kCk;  // steps per segment = checkpoint interval
   constexpr int HS = 8;     // states per half
@@ -160,19 +168,21 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const bool active = dloc < Dg;
   const int64_t d0 = g * Dg + j * kWave;
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int c = (int)bp.y;
+  const int c = (int)(bp.y % p.K);
+  const int gn = MULTI ? (int)(bp.y / p.K) : 0;  // state group
+  const int s0 = gn * NS;                         // its first state
   const int t0 = c * (int)p.Lc;
   const int t1 = min(t0 + (int)p.Lc, (int)p.L);
-  const int N = (int)p.N;
+  const int N = (int)p.N - s0;                    // states of the group (may exceed NS)
   const int64_t ch = b * p.D + d;
   const bool varlen = p.nseq > 0;
 
   float Ap[NS], gs[NS], dAacc[NS];
   {
-    const float* gin = p.ws_g + (ch * p.K + c) * p.N;
+    const float* gin = p.ws_g + (ch * p.K + c) * p.N + s0;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
-      Ap[n] = (n < N) ? p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e : 0.f;
+      Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
       gs[n] = (n < N && p.K > 1) ? gin[n] : 0.f;
       dAacc[n] = 0.f;
     }
@@ -203,12 +213,14 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const uint32_t st_y = HAS_Z ? (uint32_t)(p.sout[2] * ES) : 0u;
   const uint32_t st_dz = HAS_Z ? (uint32_t)(p.sdz[2] * ES) : 0u;
 
-  const char* const Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3]) * EB;
-  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const char* const Bbase =
+      (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3] + s0) * EB;
+  const char* const Cbase =
+      (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3] + s0) * EB;
   const uint32_t Bst = (uint32_t)(p.sB[3] * EB), Cst = (uint32_t)(p.sC[3] * EB);
-  float* const pBrow = p.ws_pB + ((b * p.G + g) * p.nJ + j) * p.L * kPartRow;
-  float* const pCrow = p.ws_pC + ((b * p.G + g) * p.nJ + j) * p.L * kPartRow;
-  const float* const xck = p.x_ckpt + (b * p.nck * p.D + d) * p.N;  // [b, k, d, :]
+  float* const pBrow = p.ws_pB + ((b * p.G + g) * p.nJ + j) * p.L * p.NPr + s0;
+  float* const pCrow = p.ws_pC + ((b * p.G + g) * p.nJ + j) * p.L * p.NPr + s0;
+  const float* const xck = p.x_ckpt + (b * p.nck * p.D + d) * p.N + s0;  // [b, k, d, s0:]
   const int64_t xck_step = p.D * p.N;
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
@@ -254,7 +266,7 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
         // out_z = out * silu(z):  dy = dout silu(z),  dz = dout out sig (1 + z (1 - sig))
         const float zz = zn[i], sg = sigmoidf_(zz);
         dy[i] = on[i] * (zz * sg);
-        if (ts + i < te)
+        if (ts + i < te && gn == 0)
           Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz,
                           on[i] * yn[i] * sg * (1.f + zz * (1.f - sg)));
       }
@@ -349,8 +361,8 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
           wave_transpose_reduce8(pC, lane);
           const int nn = hh * HS + ((lane >> 3) & 7);
           if ((lane & 7) == 0 && nn < N) {
-            pBrow[(int64_t)t * kPartRow + nn] = pB[0];
-            pCrow[(int64_t)t * kPartRow + nn] = pC[0];
+            pBrow[(int64_t)t * p.NPr + nn] = pB[0];
+            pCrow[(int64_t)t * p.NPr + nn] = pC[0];
           }
         }
       }
@@ -358,6 +370,15 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
     // Per-step outputs of the segment.
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
+      if (MULTI) {  // this group's sums over states; du / ddelta are formed by bwd_finish
+        if (ts + i < te && active) {
+          const int64_t o = (((int64_t)gn * p.Bsz + b) * p.L + ts + i) * p.D + d;
+          p.ws_s1[o] = s1[i];
+          p.ws_s2[o] = s2[i];
+          dDacc = fmaf(dy[i], uu[i], dDacc);
+        }
+        continue;
+      }
       if (ts + i < te) {
         const uint32_t r = (uint32_t)(ts + i - t0);
         const float duv = fmaf(dt[i], s1[i], Dv * dy[i]);
@@ -372,52 +393,117 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   }
   if (active) {
     const int64_t row = b * p.K + c;
-    float* dAp = p.ws_dA + (row * p.D + d) * p.N;
+    float* dAp = p.ws_dA + (row * p.D + d) * p.N + s0;
 #pragma unroll
     for (int n = 0; n < NS; ++n)
       if (n < N) dAp[n] = dAacc[n];
-    if (p.has_D) p.ws_dD[row * p.D + d] = dDacc;
-    if (p.has_bias) p.ws_db[row * p.D + d] = dbacc;
+    if (p.has_D && gn == 0) p.ws_dD[row * p.D + d] = dDacc;
+    if (p.has_bias && !MULTI) p.ws_db[row * p.D + d] = dbacc;
   }
+}
+
+// dstate > 16: du = Delta S1 + D dy and dDelta = u S1 + S2 (times softplus'), with S1, S2 the
+// sums over all state groups of ws_s1 / ws_s2; also the ddelta_bias partials.  One wave per
+// (batch, 64 channels, chunk), lane = channel.
+template <typename Tio, int DTM, bool HAS_Z>
+__global__ void __launch_bounds__(kWave) bwd_finish(BwdK p) {
+  constexpr int ES = Elem<Tio>::kSize;
+  const int lane = threadIdx.x;
+  const BlockPos bp = block_pos(p.Bsz * p.nDblk);
+  const int64_t Dg = p.D / p.G;
+  const int64_t b = bp.x / p.nDblk;
+  const int64_t rem = bp.x % p.nDblk;
+  const int64_t g = rem / p.nJ;
+  const int64_t j = rem % p.nJ;
+  const int64_t dloc = j * kWave + lane;
+  const bool active = dloc < Dg;
+  const int64_t d0 = g * Dg + j * kWave;
+  const int64_t d = g * Dg + (active ? dloc : Dg - 1);
+  const int c = (int)bp.y;
+  const int t0 = c * (int)p.Lc;
+  const int t1 = min(t0 + (int)p.Lc, (int)p.L);
+  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
+  const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
+  auto rsrc = [&](const void* base, const int64_t* s) {
+    return make_rsrc((const char*)base + (b * s[0] + d0 * s[1] + (int64_t)t0 * s[2]) * ES);
+  };
+  auto voff = [&](const int64_t* s) { return active ? (uint32_t)(lane * s[1] * ES) : kOffDrop; };
+  const auto rs_u = rsrc(p.u, p.su), rs_d = rsrc(p.delta, p.sdl), rs_o = rsrc(p.dout, p.sdo);
+  const auto rs_du = rsrc(p.du, p.sdu), rs_dd = rsrc(p.ddelta, p.sddl);
+  const auto rs_z = rsrc(HAS_Z ? p.z : p.u, HAS_Z ? p.sz : p.su);
+  const uint32_t vo_u = voff(p.su), vo_d = voff(p.sdl), vo_o = voff(p.sdo), vo_du = voff(p.sdu);
+  const uint32_t vo_dd = voff(p.sddl), vo_z = HAS_Z ? voff(p.sz) : kOffDrop;
+  float dbacc = 0.f;
+  for (int t = t0; t < t1; ++t) {
+    const uint32_t r = (uint32_t)(t - t0);
+    const float uu = Buf<Tio>::load(rs_u, vo_u, r * (uint32_t)(p.su[2] * ES));
+    const float raw = Buf<Tio>::load(rs_d, vo_d, r * (uint32_t)(p.sdl[2] * ES));
+    float dy = Buf<Tio>::load(rs_o, vo_o, r * (uint32_t)(p.sdo[2] * ES));
+    if (HAS_Z) {
+      const float zz = Buf<Tio>::load(rs_z, vo_z, r * (uint32_t)(p.sz[2] * ES));
+      dy *= zz * sigmoidf_(zz);
+    }
+    float s1 = 0.f, s2 = 0.f;
+    for (int64_t gn = 0; gn < p.nsg; ++gn) {
+      const int64_t o = ((gn * p.Bsz + b) * p.L + t) * p.D + d;
+      s1 += p.ws_s1[o];
+      s2 += p.ws_s2[o];
+    }
+    const float dt = prep_dt<DTM>(raw, bias);
+    const float duv = fmaf(dt, s1, Dv * dy);
+    float ddv = fmaf(uu, s1, s2 * 0.69314718055994531f);  // Ap = A log2(e)
+    if (DTM == kDtSoftplus) ddv *= softplus20_grad(raw + bias);
+    Buf<Tio>::store(rs_du, vo_du, r * (uint32_t)(p.sdu[2] * ES), duv);
+    Buf<Tio>::store(rs_dd, vo_dd, r * (uint32_t)(p.sddl[2] * ES), ddv);
+    dbacc += ddv;
+  }
+  if (active && p.has_bias) p.ws_db[(b * p.K + c) * p.D + d] = dbacc;
 }
 
 // ---------------------------------------------------------------------------------------
 
-template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI>
 static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st, void* const* ev) {
   hipError_t e;
   const int64_t nx = k.Bsz * k.nDblk;
   if (k.K > 1) {
-    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, k.K - 1), dim3(kWave),
-                       0, st, k);
+    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, (k.K - 1) * k.nsg),
+                       dim3(kWave), 0, st, k);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_bwd_carry(k, st)) != hipSuccess) return e;
   }
   if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, k.K), dim3(kWave), 0, st, k);
+  hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K * k.nsg),
+                     dim3(kWave), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if ((e = record_event(ev, 1, st)) != hipSuccess) return e;
+  if (MULTI) {
+    hipLaunchKernelGGL((bwd_finish<Tio, DTM, HAS_Z>), xcd_grid(nx, k.K), dim3(kWave), 0, st, k);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   return launch_bwd_reduce(k, st);
 }
 
-template <typename Tio, typename Tbc, int NS, int DTM>
+template <typename Tio, typename Tbc, int NS, int DTM, bool MULTI>
 static hipError_t launch_bwd_z(const BwdK& k, hipStream_t st, void* const* ev) {
-  return k.has_z ? launch_bwd_t<Tio, Tbc, NS, DTM, true>(k, st, ev)
-                 : launch_bwd_t<Tio, Tbc, NS, DTM, false>(k, st, ev);
+  return k.has_z ? launch_bwd_t<Tio, Tbc, NS, DTM, true, MULTI>(k, st, ev)
+                 : launch_bwd_t<Tio, Tbc, NS, DTM, false, MULTI>(k, st, ev);
 }
 
-template <typename Tio, typename Tbc, int NS>
+template <typename Tio, typename Tbc, int NS, bool MULTI>
 static hipError_t launch_bwd_dt(const BwdK& k, hipStream_t st, void* const* ev) {
   switch (dt_mode(k.has_bias, k.softplus)) {
-    case kDtRaw: return launch_bwd_z<Tio, Tbc, NS, kDtRaw>(k, st, ev);
-    case kDtBias: return launch_bwd_z<Tio, Tbc, NS, kDtBias>(k, st, ev);
-    default: return launch_bwd_z<Tio, Tbc, NS, kDtSoftplus>(k, st, ev);
+    case kDtRaw: return launch_bwd_z<Tio, Tbc, NS, kDtRaw, MULTI>(k, st, ev);
+    case kDtBias: return launch_bwd_z<Tio, Tbc, NS, kDtBias, MULTI>(k, st, ev);
+    default: return launch_bwd_z<Tio, Tbc, NS, kDtSoftplus, MULTI>(k, st, ev);
   }
 }
 
 template <typename Tio, typename Tbc>
 static hipError_t launch_bwd_bc(const BwdK& k, hipStream_t st, void* const* ev) {
-  return k.N <= 8 ? launch_bwd_dt<Tio, Tbc, 8>(k, st, ev) : launch_bwd_dt<Tio, Tbc, 16>(k, st, ev);
+  if (k.N <= 8) return launch_bwd_dt<Tio, Tbc, 8, false>(k, st, ev);
+  if (k.N <= 16) return launch_bwd_dt<Tio, Tbc, 16, false>(k, st, ev);
+  return launch_bwd_dt<Tio, Tbc, 16, true>(k, st, ev);
 }
 
 template <typename Tio>

@@ -67,19 +67,23 @@ struct BwdK {
   float* ws_g;   // [Bsz*D, K, N]     reverse chunk summaries, then carried-in gradients
   float* ws_s;   // [Bsz*D, K]        sum of Delta over each chunk
   int32_t* ws_r; // [Bsz*D, K]        1 if a sequence starts inside the chunk (varlen only)
-  float* ws_pB;  // [Bsz, G, nJ, L, kPartRow]  per-64-channel-block partial dB
-  float* ws_pC;  // [Bsz, G, nJ, L, kPartRow]  per-64-channel-block partial dC
+  float* ws_pB;  // [Bsz, G, nJ, L, NPr]  per-64-channel-block partial dB
+  float* ws_pC;  // [Bsz, G, nJ, L, NPr]  per-64-channel-block partial dC
+  float* ws_s1;  // [nsg, Bsz, L, D]  dstate > 16: per-state-group sum of lambda B
+  float* ws_s2;  // [nsg, Bsz, L, D]  dstate > 16: per-state-group sum of q A
   float* ws_dA;  // [Bsz*K, D, N]     per-(batch, chunk) partial dA
   float* ws_dD;  // [Bsz*K, D]        per-(batch, chunk) partial dD
   float* ws_db;  // [Bsz*K, D]        per-(batch, chunk) partial ddelta_bias
   int64_t K, Lc;
   int64_t nDblk;   // G * nJ: 64-channel blocks per batch
   int64_t nJ;      // ceil(Dg / 64)
+  int64_t nsg;     // state groups of 16 (1 when dstate <= 16)
+  int64_t NPr;     // row width of the dB / dC partials (16 * nsg, zero-padded)
   int32_t has_D, has_z, has_bias, softplus;
 };
 
-// Row width of the backward's partial dB / dC buffers (dstate <= 16, zero-padded rows).
-constexpr int kPartRow = 16;
+// States per group of the backward kernels (a dstate above it is split into groups).
+constexpr int kBwdGroup = 16;
 
 // Parameter block of the inter-chunk carry kernels.
 struct CarryK {

@@ -50,32 +50,36 @@ __global__ void __launch_bounds__(256) chunk_carry(CarryK p) {
 }
 
 // dB[b, g, n, t] (dC likewise) = sum over the 64-channel blocks j of the partials
-// ws_pB[b, g, j, t, 0:16]; one thread per (b, g, t), fixed summation order.
+// ws_pB[b, g, j, t, 0:NPr]; one thread per (b, g, t), fixed summation order.
 __global__ void __launch_bounds__(256) bwd_reduce_bc(BwdK p) {
+  constexpr int W = kBwdGroup;
   const int64_t total = p.Bsz * p.G * p.L;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i % p.L;
     const int64_t bg = i / p.L;
     const int64_t b = bg / p.G, g = bg % p.G;
-    float sb[kPartRow], sc[kPartRow];
+    for (int64_t n0 = 0; n0 < p.NPr; n0 += W) {
+      float sb[W], sc[W];
 #pragma unroll
-    for (int n = 0; n < kPartRow; ++n) sb[n] = sc[n] = 0.f;
-    for (int64_t j = 0; j < p.nJ; ++j) {
-      const int64_t row = ((bg * p.nJ + j) * p.L + t) * kPartRow;
+      for (int n = 0; n < W; ++n) sb[n] = sc[n] = 0.f;
+      for (int64_t j = 0; j < p.nJ; ++j) {
+        const int64_t row = ((bg * p.nJ + j) * p.L + t) * p.NPr + n0;
 #pragma unroll
-      for (int n = 0; n < kPartRow; n += 4) {
-        const float4 vb = *reinterpret_cast<const float4*>(p.ws_pB + row + n);
-        const float4 vc = *reinterpret_cast<const float4*>(p.ws_pC + row + n);
-        sb[n] += vb.x; sb[n + 1] += vb.y; sb[n + 2] += vb.z; sb[n + 3] += vb.w;
-        sc[n] += vc.x; sc[n + 1] += vc.y; sc[n + 2] += vc.z; sc[n + 3] += vc.w;
+        for (int n = 0; n < W; n += 4) {
+          const float4 vb = *reinterpret_cast<const float4*>(p.ws_pB + row + n);
+          const float4 vc = *reinterpret_cast<const float4*>(p.ws_pC + row + n);
+          sb[n] += vb.x; sb[n + 1] += vb.y; sb[n + 2] += vb.z; sb[n + 3] += vb.w;
+          sc[n] += vc.x; sc[n + 1] += vc.y; sc[n + 2] += vc.z; sc[n + 3] += vc.w;
+        }
       }
-    }
 #pragma unroll
-    for (int n = 0; n < kPartRow; ++n) {
-      if (n < p.N) {
-        p.dB[b * p.sdB[0] + g * p.sdB[1] + n * p.sdB[2] + t * p.sdB[3]] = sb[n];
-        p.dC[b * p.sdC[0] + g * p.sdC[1] + n * p.sdC[2] + t * p.sdC[3]] = sc[n];
+      for (int n = 0; n < W; ++n) {
+        const int64_t nn = n0 + n;
+        if (nn < p.N) {
+          p.dB[b * p.sdB[0] + g * p.sdB[1] + nn * p.sdB[2] + t * p.sdB[3]] = sb[n];
+          p.dC[b * p.sdC[0] + g * p.sdC[1] + nn * p.sdC[2] + t * p.sdC[3]] = sc[n];
+        }
       }
     }
   }

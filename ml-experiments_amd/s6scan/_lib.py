@@ -17,7 +17,7 @@ import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 ABI_VERSION = 2
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
-MAX_DSTATE_BWD = 16
+MAX_DSTATE_BWD = 64
 
 F32, BF16, F16 = 0, 1, 2
 OK, E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_HIP = 0, -1, -2, -3, -4

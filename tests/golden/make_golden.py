@@ -23,8 +23,9 @@ CASES = {
     "fp32_groups_z_bias": (2, 40, 128, 8, 2, "fp32", True, True, None, True),
     "bf16_dense": (1, 130, 64, 16, 1, "bf16", False, False, None, True),
     "fp32_varlen": (1, 200, 64, 16, 1, "fp32", True, True, [0, 37, 38, 150, 200], True),
-    "fp32_n64": (1, 50, 64, 64, 1, "fp32", False, False, None, False),
+    "fp32_n64": (1, 50, 64, 64, 1, "fp32", False, False, None, True),
     "fp32_n12": (2, 33, 64, 12, 1, "fp32", True, False, None, True),
+    "fp32_n24_varlen": (1, 90, 64, 24, 1, "fp32", True, True, [0, 30, 31, 90], True),
 }
 
 

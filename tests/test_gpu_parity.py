@@ -176,6 +176,11 @@ BWD_CASES = [
     (2, 90, 512, 16, torch.float32, 2, False, False),
     (1, 31, 300, 16, torch.float32, 1, False, False),
     (1, 1, 64, 16, torch.float32, 1, True, True),
+    # dstate > 16: the backward splits the states into groups of 16
+    (2, 150, 128, 24, torch.float32, 1, True, True),
+    (1, 100, 64, 32, torch.bfloat16, 1, False, False),
+    (2, 77, 96, 64, torch.float32, 2, False, True),
+    (1, 300, 64, 48, torch.float16, 1, True, False),
 ]
 
 
