@@ -46,26 +46,33 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="fwd1",
-                    choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "copyref"])
+                    choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
 
-def cpu_baseline(cfg, make_inputs):
-    """Reference CPU path (torch restatement of selective_scan_ref) on a bounded sample:
-    one sequence of the workload (4096 steps forward, 2048 steps forward + backward)."""
+def cpu_baseline(cfg, make_inputs, mixer=False):
+    """Reference CPU path on a bounded sample: one sequence of the workload (4096 steps
+    forward, 2048 steps forward + backward).  The scan workloads time the torch restatement
+    of selective_scan_ref (op for op); the mixer workload the restatement of the reference
+    SSMMixer's own scan loop (backbone.py:1207-1242, state in the input dtype as there)."""
     import dataclasses
 
     import torch
     from oracle.selective_scan_ref import selective_scan_ref, selective_scan_ref_grads
+    from oracle.ssm_mixer_ref import ssm_mixer_scan_ref
     torch.set_num_threads(os.cpu_count() or 1)
     seqlen = 2048 if (cfg.backward or not cfg.seqlen) else min(cfg.seqlen, 4096)
     sample = dataclasses.replace(cfg, batch=1, seqlen=seqlen, nseq=0)
     inp = make_inputs(sample)
     args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
+    mix = mixer_extras(torch, inp, torch.Generator("cpu").manual_seed(7)) if mixer else None
 
     def run():
-        if sample.backward:
+        if mixer:
+            ssm_mixer_scan_ref(inp["x"], mix["dt_raw"], mix["A_log"], mix["B"], mix["C"],
+                               inp["D"], mix["z"])
+        elif sample.backward:
             selective_scan_ref_grads(*args, inp["D"], inp["dy"].mT)
         else:
             selective_scan_ref(*args, D=inp["D"], return_last_state=True)
@@ -82,12 +89,31 @@ def cpu_baseline(cfg, make_inputs):
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"restated reference CPU path (selective_scan_ref op for op"
+        "sample": (f"restated reference CPU path ("
+                   f"{'SSMMixer scan loop' if mixer else 'selective_scan_ref'} op for op"
                    f"{' + autograd backward' if sample.backward else ''}) on one sequence of "
                    f"{cfg.name}: batch 1, seqlen {seqlen}, dim {cfg.dim}, dstate {cfg.dstate}; "
                    f"median of 3 runs = {sec:.3f} s; os.cpu_count() = {os.cpu_count()}"),
         "mtok_ch_per_s": round(seqlen * cfg.dim / sec / 1e6, 4),
     }
+
+
+def mixer_extras(torch, inp, g):
+    """Inputs of the SSMMixer-shaped workload, derived from a scan workload's inputs the
+    way the reference mixer produces them (backbone.py:1185-1209): z is the second half of
+    the in_proj output, B and C are slices of the x_proj output [B, L, dt_rank + 2N], dt is
+    the dt_proj output before softplus, A = -exp(A_log)."""
+    Bsz, L, D = inp["x"].shape
+    N = inp["A"].shape[1]
+    R = 16
+    dev, dt = inp["x"].device, inp["x"].dtype
+    xz = torch.randn(Bsz, L, 2 * D, generator=g).to(dt).to(dev)
+    params = torch.empty(Bsz, L, R + 2 * N, dtype=dt, device=dev)
+    params[..., R:R + N] = inp["B"]
+    params[..., R + N:] = inp["C"]
+    dt_raw = (0.5 * torch.randn(Bsz, L, D, generator=g) - 1.0).to(dt).to(dev)
+    return {"z": xz.chunk(2, dim=-1)[1], "B": params[..., R:R + N], "C": params[..., R + N:],
+            "dt_raw": dt_raw, "A_log": torch.log(-inp["A"])}
 
 
 def copy_reference(torch, steps):
@@ -122,7 +148,8 @@ def main():
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
 
     cfg = {"fwd1": CONFIGS[1], "fwdbwd3": CONFIGS[3], "fwd2": CONFIGS[2],
-           "fwdbwd4": CONFIGS[4]}[args.workload]
+           "fwdbwd4": CONFIGS[4], "mixer1": CONFIGS[1]}[args.workload]
+    mixer = args.workload == "mixer1"
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
@@ -132,17 +159,27 @@ def main():
     import dataclasses
     for s in range(nsets):
         cpu = make_inputs(dataclasses.replace(cfg, seed=cfg.seed + 1000 * s))
-        sets.append({k: v.to(dev) for k, v in cpu.items()})
+        st = {k: v.to(dev) for k, v in cpu.items()}
+        if mixer:
+            st.update(mixer_extras(torch, st, torch.Generator("cpu").manual_seed(77 + s)))
+        sets.append(st)
         del cpu
     L = sets[0]["x"].shape[1]
     B = sets[0]["x"].shape[0]
     nbytes = cfg.algorithmic_bytes(seqlen=L)
+    if mixer:  # + z read, + the gated output written next to the pre-gate one
+        nbytes += 2 * B * L * cfg.dim * sets[0]["x"].element_size()
 
     def step(i, ev=None, ev_b=None):
         g = sets[i % nsets]
         a = (g["x"].mT, g["delta"].mT, g["A"], g["B"].mT, g["C"].mT)
         cu = g.get("cu_seqlens")
-        if not cfg.backward:
+        if mixer:  # the SSMMixer S6 core as s6scan.ssm_mixer.ssm_mixer_scan issues it
+            with torch.no_grad():
+                selective_scan_forward(g["x"].mT, g["dt_raw"].mT, -torch.exp(g["A_log"]),
+                                       g["B"].mT, g["C"].mT, D=g["D"], z=g["z"].mT,
+                                       delta_softplus=True, want_ckpt=False, kernel_events=ev)
+        elif not cfg.backward:
             with torch.no_grad():
                 selective_scan_forward(*a, D=g["D"], cu_seqlens=cu, want_ckpt=False,
                                        want_last_state=True, kernel_events=ev)
@@ -211,8 +248,10 @@ def main():
         "dtype": "f32",
         "io_dtype": str(cfg.dtype).replace("torch.", ""),
         "data": "synthetic (seeded normal/uniform inputs of the workload's shape; 3 rotating sets)",
-        "config": {"workload": f"{cfg.name}: selective_scan_fn {'fwd+bwd' if cfg.backward else 'fwd'}"
-                               " on channel-last [B, L, D] views",
+        "config": {"workload": (f"{cfg.name}: SSMMixer S6 core (softplus, D skip, z gate fused; "
+                                "B/C slices of x_proj output)" if mixer else
+                                f"{cfg.name}: selective_scan_fn {'fwd+bwd' if cfg.backward else 'fwd'}"
+                                " on channel-last [B, L, D] views"),
                    "batch": B, "seqlen": L, "dim": cfg.dim, "dstate": cfg.dstate,
                    "nseq": cfg.nseq, "algorithmic_bytes_per_step": nbytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 5),
@@ -236,7 +275,7 @@ def main():
         res["fwd_kernel_ms"] = round(k_ms, 5)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(cfg, make_inputs)
+        res["cpu_baseline"] = cpu_baseline(cfg, make_inputs, mixer=mixer)
     print(json.dumps(res), flush=True)
 
 

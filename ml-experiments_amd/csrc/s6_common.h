@@ -167,15 +167,41 @@ template <typename T> constexpr int kGroupStates = 32 / Elem<T>::kSize;
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// F.softplus with beta=1, threshold=20 (selective_scan_interface.py:111-112).
-__device__ inline float softplus20(float x) { return x <= 20.f ? log1pf(expf(x)) : x; }
-// d softplus / dx, matching torch's softplus_backward (exp(x)/(exp(x)+1) below threshold).
-__device__ inline float softplus20_grad(float x) {
-  if (x > 20.f) return 1.f;
-  float e = expf(x);
-  return e / (e + 1.f);
+constexpr float kLog2eLo = 1.925963033500011e-08f;  // log2(e) - (float)log2(e)
+constexpr float kLn2 = 0.69314718055994531f;
+
+// e^x from the hardware exp2 with the exponent x log2(e) carried as hi + lo, so the
+// rounding of the product does not reach the result (a few ulp for |x| < 88).
+__device__ inline float exp_split(float x) {
+  const float p = x * kLog2e;
+  const float lo = fmaf(x, kLog2eLo, fmaf(x, kLog2e, -p));
+  const float e = fast_exp2(p);
+  return fmaf(e, lo * kLn2, e);
 }
-__device__ inline float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// F.softplus with beta=1, threshold=20 (selective_scan_interface.py:111-112): x above 20,
+// else log(1 + e^x), evaluated as max(x, 0) + log1p(e^-|x|) with the hardware log2 and
+// log1p(t) = ln(u) t / (u - 1), u = 1 + t, which cancels the rounding of 1 + t.  Within
+// 4 ulp of torch's fp32 softplus (float32 emulation over 3e5 points in [-30, 25]).
+__device__ inline float softplus20(float x) {
+  const float t = exp_split(-fabsf(x));
+  const float u = 1.f + t;
+  const float um1 = u - 1.f;
+  const float lp =
+      um1 == 0.f ? t : (__builtin_amdgcn_logf(u) * kLn2) * (t * __builtin_amdgcn_rcpf(um1));
+  const float sp = fmaxf(x, 0.f) + lp;
+  return x > 20.f ? x : sp;
+}
+// d softplus / dx as torch's softplus_backward: e^x / (e^x + 1) below the threshold, else 1.
+__device__ inline float softplus20_grad(float x) {
+  const float e = exp_split(fminf(x, 20.f));
+  const float g = e * __builtin_amdgcn_rcpf(e + 1.f);
+  return x > 20.f ? 1.f : g;
+}
+// 1 / (1 + e^-x)  (silu(z) = z sigmoid(z), SSI:154-155)
+__device__ inline float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.f + exp_split(-x));
+}
 
 // How Delta is formed from the delta input (selective_scan_interface.py:107-112): as is,
 // plus delta_bias, or softplus(delta + delta_bias) (bias 0 when absent).

@@ -288,3 +288,22 @@ def test_golden_fixtures_reproduced_by_restatement(name):
                                      t("delta_bias"), sp, True, compute_dtype=F64)
     np.testing.assert_allclose(out.numpy(), d["ref_out"], rtol=1e-11, atol=1e-11)
     np.testing.assert_allclose(ls.numpy(), d["ref_last_state"], rtol=1e-11, atol=1e-11)
+
+
+def test_ssm_mixer_restatement_matches_selective_scan_ref():
+    """The SSMMixer loop (backbone.py:1207-1242) and selective_scan_ref (SSI:91-157) are the
+    same recurrence in two layouts: with softplus on dt, D skip and z gate they agree to
+    float64 rounding."""
+    from oracle.ssm_mixer_ref import ssm_mixer_scan_ref
+    g = torch.Generator().manual_seed(21)
+    B, L, I, N = 2, 40, 24, 8
+    f64 = dict(generator=g, dtype=torch.float64)
+    x_conv, dt_lin, z = (torch.randn(B, L, I, **f64) for _ in range(3))
+    A_log = torch.log(torch.arange(1, N + 1, dtype=torch.float64))[None].repeat(I, 1)
+    A_log = A_log + 0.1 * torch.randn(I, N, **f64)
+    Bp, Cp = torch.randn(B, L, N, **f64), torch.randn(B, L, N, **f64)
+    Dv = torch.randn(I, **f64)
+    y1 = ssm_mixer_scan_ref(x_conv, dt_lin, A_log, Bp, Cp, Dv, z)
+    y2 = selective_scan_ref(x_conv.mT, dt_lin.mT, -torch.exp(A_log), Bp.mT, Cp.mT, D=Dv, z=z.mT,
+                            delta_softplus=True, compute_dtype=torch.float64).mT
+    assert torch.allclose(y1, y2, rtol=1e-12, atol=1e-12)
