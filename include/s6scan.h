@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define S6_ABI_VERSION 2
+#define S6_ABI_VERSION 3
 #define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
 #define S6_MAX_DSTATE_BWD 64
@@ -115,6 +115,9 @@ typedef struct S6BwdArgs {
   float* dC;                int64_t dC_stride[4];
   float* dD;                int64_t dD_stride;        /* has_D only                     */
   void* dz;                 int64_t dz_stride[3];     /* has_z only                     */
+  /* Optional (NULL = not written; has_z only): out * silu(z) recomputed from out and z, the
+   * reference's recompute_out_z (selective_scan_interface.py:263-267). */
+  void* out_z;              int64_t out_z_stride[3];
   float* ddelta_bias;       int64_t ddelta_bias_stride; /* has_delta_bias only          */
   void* workspace;          size_t workspace_bytes;
   void* kernel_events[2];   /* as in S6FwdArgs, around the main backward kernel          */

@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <string>
 
 #include "s6_internal.h"
@@ -207,9 +208,143 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   return k;
 }
 
+// ---- causal conv1d ---------------------------------------------------------------------
+
+constexpr int64_t kConvT = 64;            // steps per wave tile
+constexpr int64_t kConvTargetBlocks = 2048;
+
+struct ConvPlan {
+  int64_t T, ntile4, nsplit, tps;
+  size_t ws_bytes;
+};
+
+ConvPlan conv_plan(const S6ConvProblem& p) {
+  ConvPlan c;
+  c.T = kConvT;
+  c.ntile4 = ceil_div(p.seqlen, 4 * kConvT);
+  // Backward blocks along the sequence: enough (batch, 256-channel, split) blocks to fill
+  // the chip; every block writes one partial row, so no more than that.
+  const int64_t per = p.batch * ceil_div(p.dim, 256);
+  int64_t ns = std::min(c.ntile4, std::max<int64_t>(1, ceil_div(kConvTargetBlocks, per)));
+  c.tps = ceil_div(c.ntile4, ns);
+  c.nsplit = ceil_div(c.ntile4, c.tps);
+  c.ws_bytes = (size_t)(p.batch * c.nsplit * p.dim * (p.width + 1)) * 4;
+  return c;
+}
+
+// Channels per lane: 16 bytes of channel-contiguous storage when every tensor allows it.
+bool conv_vec_ok(const void* ptr, const int64_t s[3], int64_t vec, int es) {
+  return s[1] == 1 && s[0] % vec == 0 && s[2] % vec == 0 &&
+         ((uintptr_t)ptr % (uintptr_t)(vec * es)) == 0;
+}
+
+int conv_check_problem(const S6ConvProblem& p) {
+  if (p.batch < 1 || p.dim < 1 || p.seqlen < 1)
+    return fail(S6_E_INVALID, "causal_conv1d: batch, dim, seqlen must be >= 1");
+  if (p.width < 2 || p.width > S6_CONV_MAX_WIDTH)
+    return fail(S6_E_UNSUPPORTED, "causal_conv1d: width must be in [2, %d], got %lld",
+                S6_CONV_MAX_WIDTH, (long long)p.width);
+  if (p.io_dtype != S6_F32 && p.io_dtype != S6_BF16 && p.io_dtype != S6_F16)
+    return fail(S6_E_INVALID, "causal_conv1d: bad io_dtype %d", p.io_dtype);
+  if (p.silu != 0 && p.silu != 1) return fail(S6_E_INVALID, "causal_conv1d: silu must be 0 or 1");
+  if (ceil_div(p.seqlen, 4 * kConvT) > 65535)
+    return fail(S6_E_UNSUPPORTED, "causal_conv1d: seqlen %lld too long", (long long)p.seqlen);
+  if (p.batch * p.dim > ((int64_t)1 << 31) - 1)
+    return fail(S6_E_UNSUPPORTED, "causal_conv1d: batch * dim too large");
+  return S6_OK;
+}
+
+int conv_check_common(const S6ConvProblem& p, const void* x, const int64_t* sx, const float* w,
+                      const int64_t* sw) {
+  int r;
+  if ((r = conv_check_problem(p))) return r;
+  if ((r = check_ptr(x, "x")) || (r = check_strides(sx, 3, "x")) || (r = check_ptr(w, "weight")) ||
+      (r = check_strides(sw, 2, "weight")))
+    return r;
+  return S6_OK;
+}
+
+s6::ConvK conv_fill(const S6ConvProblem& p, const ConvPlan& c, int64_t vec) {
+  s6::ConvK k{};
+  k.Bsz = p.batch; k.D = p.dim; k.L = p.seqlen;
+  k.T = c.T; k.ntile4 = c.ntile4; k.nsplit = c.nsplit; k.tps = c.tps;
+  k.nCb = ceil_div(p.dim, 64 * vec);
+  return k;
+}
+
 }  // namespace
 
 extern "C" {
+
+int s6_causal_conv1d_validate_fwd(const S6ConvFwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  int r;
+  if ((r = conv_check_common(a->p, a->x, a->x_stride, a->weight, a->weight_stride)) ||
+      (r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 3, "out")))
+    return r;
+  return ok();
+}
+
+int s6_causal_conv1d_validate_bwd(const S6ConvBwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  int r;
+  if ((r = conv_check_common(a->p, a->x, a->x_stride, a->weight, a->weight_stride)) ||
+      (r = check_ptr(a->dout, "dout")) || (r = check_strides(a->dout_stride, 3, "dout")) ||
+      (r = check_ptr(a->dx, "dx")) || (r = check_strides(a->dx_stride, 3, "dx")) ||
+      (r = check_ptr(a->dweight, "dweight")) || (r = check_strides(a->dweight_stride, 2, "dweight")))
+    return r;
+  const ConvPlan c = conv_plan(a->p);
+  if (a->workspace == nullptr || a->workspace_bytes < c.ws_bytes)
+    return fail(S6_E_WORKSPACE, "causal_conv1d backward workspace needs %zu bytes, got %zu",
+                c.ws_bytes, a->workspace ? a->workspace_bytes : (size_t)0);
+  return ok();
+}
+
+size_t s6_causal_conv1d_bwd_workspace_bytes(const S6ConvProblem* p) {
+  if (p == nullptr || conv_check_problem(*p) != S6_OK) return 0;
+  return conv_plan(*p).ws_bytes;
+}
+
+int s6_causal_conv1d_fwd(const S6ConvFwdArgs* a, void* stream) {
+  int r = s6_causal_conv1d_validate_fwd(a);
+  if (r != S6_OK) return r;
+  const S6ConvProblem& p = a->p;
+  const int es = esize(p.io_dtype);
+  const int64_t v = 16 / es;
+  const int64_t vec = (p.dim % v == 0 && conv_vec_ok(a->x, a->x_stride, v, es) &&
+                       conv_vec_ok(a->out, a->out_stride, v, es)) ? v : 1;
+  s6::ConvK k = conv_fill(p, conv_plan(p), vec);
+  for (int i = 0; i < 3; ++i) { k.sx[i] = a->x_stride[i]; k.so[i] = a->out_stride[i]; }
+  k.sw[0] = a->weight_stride[0]; k.sw[1] = a->weight_stride[1]; k.sb = a->bias_stride;
+  k.x = a->x; k.w = a->weight; k.bias = a->bias; k.out = a->out;
+  hipError_t e = s6::launch_conv_fwd(k, p.io_dtype, (int)p.width, (int)vec, p.silu != 0,
+                                     (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_causal_conv1d_fwd: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int s6_causal_conv1d_bwd(const S6ConvBwdArgs* a, void* stream) {
+  int r = s6_causal_conv1d_validate_bwd(a);
+  if (r != S6_OK) return r;
+  const S6ConvProblem& p = a->p;
+  const int es = esize(p.io_dtype);
+  const int64_t v = 16 / es;
+  const int64_t vec = (p.dim % v == 0 && conv_vec_ok(a->x, a->x_stride, v, es) &&
+                       conv_vec_ok(a->dout, a->dout_stride, v, es) &&
+                       conv_vec_ok(a->dx, a->dx_stride, v, es)) ? v : 1;
+  s6::ConvK k = conv_fill(p, conv_plan(p), vec);
+  for (int i = 0; i < 3; ++i) {
+    k.sx[i] = a->x_stride[i]; k.sdo[i] = a->dout_stride[i]; k.sdx[i] = a->dx_stride[i];
+  }
+  k.sw[0] = a->weight_stride[0]; k.sw[1] = a->weight_stride[1]; k.sb = a->bias_stride;
+  k.sdw[0] = a->dweight_stride[0]; k.sdw[1] = a->dweight_stride[1]; k.sdb = a->dbias_stride;
+  k.x = a->x; k.w = a->weight; k.bias = a->bias; k.dout = a->dout; k.dx = a->dx;
+  k.dw = a->dweight; k.dbias = a->dbias; k.ws = (float*)a->workspace;
+  hipError_t e = s6::launch_conv_bwd(k, p.io_dtype, (int)p.width, (int)vec, p.silu != 0,
+                                     (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_causal_conv1d_bwd: %s", hipGetErrorString(e));
+  return ok();
+}
 
 int s6_abi_version(void) { return S6_ABI_VERSION; }
 
@@ -300,13 +435,16 @@ int s6_validate_bwd(const S6BwdArgs* a) {
                   (r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 3, "out"))))
     return r;
   if (p.has_delta_bias && (r = check_ptr(a->ddelta_bias, "ddelta_bias"))) return r;
+  const bool want_oz = p.has_z && a->out_z != nullptr;
+  if (want_oz && (r = check_strides(a->out_z_stride, 3, "out_z"))) return r;
   const Plan pl = make_plan(p, true, a->B, a->B_stride, a->C, a->C_stride);
   const int es = esize(p.io_dtype);
   if ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
       (r = check_span(a->dout_stride, es, pl.Lc, "dout")) || (r = check_span(a->du_stride, es, pl.Lc, "du")) ||
       (r = check_span(a->ddelta_stride, es, pl.Lc, "ddelta")) ||
       (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
-                   (r = check_span(a->dz_stride, es, pl.Lc, "dz")))))
+                   (r = check_span(a->dz_stride, es, pl.Lc, "dz")))) ||
+      (want_oz && (r = check_span(a->out_z_stride, es, pl.Lc, "out_z"))))
     return r;
   if (pl.total_bwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_bwd))
     return fail(S6_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", pl.total_bwd,
@@ -362,6 +500,7 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
       k.sout[i] = p.has_z ? a->out_stride[i] : 0;
       k.sdu[i] = a->du_stride[i]; k.sddl[i] = a->ddelta_stride[i];
       k.sdz[i] = p.has_z ? a->dz_stride[i] : 0;
+      k.soz[i] = (p.has_z && a->out_z) ? a->out_z_stride[i] : 0;
     }
     k.sA[0] = a->A_stride[0]; k.sA[1] = a->A_stride[1];
     k.sD = a->D_stride; k.sbias = a->delta_bias_stride;
@@ -388,6 +527,7 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.cu = a->cu_seqlens; k.nseq = p.nseq;
     k.x_ckpt = a->x_ckpt; k.nck = pl.nck;
     k.du = a->du; k.ddelta = a->ddelta; k.dz = a->dz;
+    k.out_z = p.has_z ? a->out_z : nullptr;
     k.dA = a->dA; k.dD = a->dD; k.dbias = a->ddelta_bias; k.dB = a->dB; k.dC = a->dC;
     k.ws_g = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
     k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;

@@ -212,6 +212,10 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const uint32_t st_z = HAS_Z ? (uint32_t)(p.sz[2] * ES) : 0u;
   const uint32_t st_y = HAS_Z ? (uint32_t)(p.sout[2] * ES) : 0u;
   const uint32_t st_dz = HAS_Z ? (uint32_t)(p.sdz[2] * ES) : 0u;
+  const bool want_oz = HAS_Z && p.out_z != nullptr;
+  const auto rs_oz = rsrc(want_oz ? p.out_z : p.du, want_oz ? p.soz : p.sdu);
+  const uint32_t vo_oz = voff(p.soz, want_oz);
+  const uint32_t st_oz = want_oz ? (uint32_t)(p.soz[2] * ES) : 0u;
 
   const char* const Bbase =
       (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3] + s0) * EB;
@@ -266,9 +270,11 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
         // out_z = out * silu(z):  dy = dout silu(z),  dz = dout out sig (1 + z (1 - sig))
         const float zz = zn[i], sg = sigmoidf_(zz);
         dy[i] = on[i] * (zz * sg);
-        if (ts + i < te && gn == 0)
+        if (ts + i < te && gn == 0) {
           Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz,
                           on[i] * yn[i] * sg * (1.f + zz * (1.f - sg)));
+          if (want_oz) Buf<Tio>::store(rs_oz, vo_oz, (uint32_t)(ts + i - t0) * st_oz, yn[i] * (zz * sg));
+        }
       }
     }
 #pragma unroll

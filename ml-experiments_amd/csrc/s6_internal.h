@@ -2,6 +2,7 @@
 // device helpers the kernel files share.
 #pragma once
 #include "s6_common.h"
+#include "causal_conv1d.h"
 
 namespace s6 {
 
@@ -62,6 +63,7 @@ struct BwdK {
   const int32_t* cu; int32_t nseq;
   const float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N], as written by the forward
   void* du; void* ddelta; void* dz;
+  void* out_z; int64_t soz[3];   // out * silu(z) (recompute_out_z), NULL: not written
   float* dA; float* dD; float* dbias; float* dB; float* dC;
   int64_t sdA[2], sdD, sdbias;
   float* ws_g;   // [Bsz*D, K, N]     reverse chunk summaries, then carried-in gradients
@@ -94,6 +96,21 @@ struct CarryK {
   int64_t nch, D, K, N;
 };
 
+// Parameter block of the causal conv1d kernels (strides in elements).
+struct ConvK {
+  int64_t Bsz, D, L;
+  int64_t sx[3], so[3], sdo[3], sdx[3];
+  int64_t sw[2], sb, sdw[2], sdb;
+  const void* x; const float* w; const float* bias; void* out;
+  const void* dout; void* dx; float* dw; float* dbias;
+  float* ws;        // backward: [Bsz * nsplit, D, W + 1] per-block dweight | dbias partials
+  int64_t T;        // steps per wave tile
+  int64_t nCb;      // channel blocks (64 lanes x VEC channels)
+  int64_t ntile4;   // blocks of 4 wave tiles along the sequence
+  int64_t nsplit;   // backward: blocks per (batch, channel block) along the sequence
+  int64_t tps;      // backward: tile blocks per split
+};
+
 inline hipError_t record_event(void* const* ev, int i, hipStream_t st) {
   if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
   return hipEventRecord((hipEvent_t)ev[i], st);
@@ -113,6 +130,11 @@ hipError_t launch_bwd_reduce(const BwdK& k, hipStream_t st);
 // ev (nullable): hipEvent_t pair recorded around the main scan kernel.
 hipError_t launch_fwd(const FwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev);
 hipError_t launch_bwd(const BwdK& k, int io_dtype, int bc_dtype, hipStream_t st, void* const* ev);
+// s6_conv.hip: causal conv1d.  vec: channels per lane (1 = any strides).
+hipError_t launch_conv_fwd(const ConvK& k, int io_dtype, int width, int vec, bool silu,
+                           hipStream_t st);
+hipError_t launch_conv_bwd(const ConvK& k, int io_dtype, int width, int vec, bool silu,
+                           hipStream_t st);
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
 hipError_t launch_relayout(const void* src, const int64_t s[4], int esize, void* dst,
                            int64_t Bsz, int64_t G, int64_t N, int64_t NP, int64_t L,

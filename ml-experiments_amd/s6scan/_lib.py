@@ -1,4 +1,4 @@
-"""ctypes binding of the s6scan C ABI (``include/s6scan.h``).
+"""ctypes binding of the s6scan C ABI (``include/s6scan.h``, ``include/causal_conv1d.h``).
 
 The shared library is built in-tree (``ml-experiments_amd/build.py``) next to this file.
 There is no fallback: if the library is missing or was built for another ABI version,
@@ -14,7 +14,7 @@ import os
 
 import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 64
@@ -85,9 +85,39 @@ class S6BwdArgs(ctypes.Structure):
         ("dC", _vp), ("dC_stride", _a(4)),
         ("dD", _vp), ("dD_stride", _i64),
         ("dz", _vp), ("dz_stride", _a(3)),
+        ("out_z", _vp), ("out_z_stride", _a(3)),
         ("ddelta_bias", _vp), ("ddelta_bias_stride", _i64),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("kernel_events", _vp * 2),
+    ]
+
+
+class S6ConvProblem(ctypes.Structure):
+    _fields_ = [("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("width", _i64),
+                ("io_dtype", _i32), ("silu", _i32)]
+
+
+class S6ConvFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("p", S6ConvProblem),
+        ("x", _vp), ("x_stride", _a(3)),
+        ("weight", _vp), ("weight_stride", _a(2)),
+        ("bias", _vp), ("bias_stride", _i64),
+        ("out", _vp), ("out_stride", _a(3)),
+    ]
+
+
+class S6ConvBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("p", S6ConvProblem),
+        ("x", _vp), ("x_stride", _a(3)),
+        ("weight", _vp), ("weight_stride", _a(2)),
+        ("bias", _vp), ("bias_stride", _i64),
+        ("dout", _vp), ("dout_stride", _a(3)),
+        ("dx", _vp), ("dx_stride", _a(3)),
+        ("dweight", _vp), ("dweight_stride", _a(2)),
+        ("dbias", _vp), ("dbias_stride", _i64),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -102,6 +132,11 @@ EXPORTS = {
     "s6_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),
     "s6_fwd": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs), ctypes.c_void_p]),
     "s6_bwd": (ctypes.c_int, [ctypes.POINTER(S6BwdArgs), ctypes.c_void_p]),
+    "s6_causal_conv1d_validate_fwd": (ctypes.c_int, [ctypes.POINTER(S6ConvFwdArgs)]),
+    "s6_causal_conv1d_validate_bwd": (ctypes.c_int, [ctypes.POINTER(S6ConvBwdArgs)]),
+    "s6_causal_conv1d_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6ConvProblem)]),
+    "s6_causal_conv1d_fwd": (ctypes.c_int, [ctypes.POINTER(S6ConvFwdArgs), ctypes.c_void_p]),
+    "s6_causal_conv1d_bwd": (ctypes.c_int, [ctypes.POINTER(S6ConvBwdArgs), ctypes.c_void_p]),
 }
 
 

@@ -117,6 +117,30 @@ def _problem(u, B, z, D, delta_bias, delta_softplus, dims):
                           int(bool(delta_softplus)), nseq)
 
 
+def _dense(t):
+    """True when t's elements exactly fill a block of memory (any dimension order)."""
+    expect = 1
+    for i in sorted(range(t.dim()), key=lambda i: t.stride(i)):
+        if t.size(i) != 1 and t.stride(i) != expect:
+            return False
+        expect *= t.size(i)
+    return True
+
+
+def _empty_like(t, u):
+    """A new tensor of t's shape and dtype in t's layout, or in u's (same shape) when t is a
+    strided view (e.g. a half of a channel-last [B, L, 2D] buffer) that empty_like would
+    turn into an L-contiguous tensor."""
+    return torch.empty_like(t) if _dense(t) else torch.empty_like(u, dtype=t.dtype)
+
+
+def _check_out(t, like, name):
+    if t.shape != like.shape or t.dtype != like.dtype or t.device != like.device:
+        raise ValueError(f"{name} must have shape {tuple(like.shape)}, dtype {like.dtype} "
+                         f"and device {like.device}")
+    return t
+
+
 def _as4(M):
     return M.unsqueeze(1) if M.dim() == 3 else M
 
@@ -174,10 +198,14 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
 
 
 def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, x_ckpt,
-                            out=None, cu_seqlens=None, kernel_events=None):
+                            out=None, cu_seqlens=None, kernel_events=None, du_out=None,
+                            dz_out=None, recompute_out_z=False):
     """One backward launch.  Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias) with dB, dC
     in B/C's own rank (3-D or 4-D) and fp32 like the reference kernel's; None for absent
-    inputs."""
+    inputs.  ``du_out`` / ``dz_out``: optional preallocated outputs of u's / z's shape and
+    dtype (any strides), as the reference kernel's ``dz`` argument (SSI:263-267).  With
+    ``recompute_out_z`` (z given) a 9th element ``out_z = out * silu(z)`` is returned, the
+    reference's recompute_out_z output."""
     dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
     batch, dim, seqlen, dstate, G, nseq = dims
     if dstate > _lib.MAX_DSTATE_BWD:
@@ -190,13 +218,16 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
     if dout.dtype != u.dtype:
         dout = dout.to(u.dtype)
     with torch.cuda.device(u.device):
-        du = torch.empty_like(u)
-        ddelta = torch.empty_like(delta)
+        du = torch.empty_like(u) if du_out is None else _check_out(du_out, u, "du_out")
+        ddelta = _empty_like(delta, u)
         dA = torch.empty(dim, dstate, dtype=torch.float32, device=u.device)
         dB4 = torch.empty(B4.shape, dtype=torch.float32, device=u.device)
         dC4 = torch.empty(C4.shape, dtype=torch.float32, device=u.device)
         dD = torch.empty(dim, dtype=torch.float32, device=u.device) if D is not None else None
-        dz = torch.empty_like(z) if z is not None else None
+        dz = None
+        if z is not None:
+            dz = _empty_like(z, u) if dz_out is None else _check_out(dz_out, z, "dz_out")
+        out_z = _empty_like(z, u) if (z is not None and recompute_out_z) else None
         dbias = (torch.empty(dim, dtype=torch.float32, device=u.device)
                  if delta_bias is not None else None)
         args = _lib.S6BwdArgs()
@@ -221,6 +252,7 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
         args.dC, args.dC_stride = _ptr(dC4), _strides(dC4, 4)
         args.dD, args.dD_stride = _ptr(dD), (dD.stride(0) if dD is not None else 0)
         args.dz, args.dz_stride = _ptr(dz), _strides(dz, 3)
+        args.out_z, args.out_z_stride = _ptr(out_z), _strides(out_z, 3)
         args.ddelta_bias = _ptr(dbias)
         args.ddelta_bias_stride = dbias.stride(0) if dbias is not None else 0
         nbytes = _lib.LIB.s6_bwd_workspace_bytes(ctypes.byref(prob))
@@ -231,6 +263,8 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
         _lib.check(_lib.LIB.s6_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "s6_bwd")
     dB = dB4.squeeze(1) if B.dim() == 3 else dB4
     dC = dC4.squeeze(1) if C.dim() == 3 else dC4
+    if out_z is not None:
+        return du, ddelta, dA, dB, dC, dD, dz, dbias, out_z
     return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 

@@ -1,6 +1,7 @@
 """The C ABI library (libs6scan.so) without a GPU: it loads, exports every entry point that
-include/s6scan.h declares, and its host-only validation rejects bad arguments with the
-documented error codes.  No compute call is made here."""
+include/*.h (s6scan.h, causal_conv1d.h) declare, and its host-only validation rejects bad
+arguments with the documented error codes.  No compute call is made here."""
+import glob
 import ctypes
 import os
 import re
@@ -11,20 +12,24 @@ from s6scan import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "s6scan.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def header_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(s6_[a-z_0-9]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b(s6_[a-z_0-9]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
     declared = header_functions()
     assert "s6_fwd" in declared and "s6_bwd" in declared
+    assert "s6_causal_conv1d_fwd" in declared and "s6_causal_conv1d_bwd" in declared
     lib = ctypes.CDLL(_lib.LIB_PATH)
     missing = [f for f in declared if not hasattr(lib, f)]
-    assert not missing, f"declared in s6scan.h but not exported: {missing}"
+    assert not missing, f"declared in include/*.h but not exported: {missing}"
     assert set(declared) == set(_lib.EXPORTS), "ctypes binding and header disagree"
 
 
@@ -138,3 +143,57 @@ def test_validate_bwd_dstate_limits():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(ImportError, match="native library not found"):
         _lib.load_library(str(tmp_path / "libs6scan.so"))
+
+
+def conv_prob(**kw):
+    d = dict(batch=2, dim=64, seqlen=300, width=4, io_dtype=_lib.BF16, silu=1)
+    d.update(kw)
+    return _lib.S6ConvProblem(**d)
+
+
+def conv_args(bwd=False, **kw):
+    a = _lib.S6ConvBwdArgs() if bwd else _lib.S6ConvFwdArgs()
+    a.p = conv_prob(**kw)
+    fake = ctypes.c_void_p(0x100000)
+    a.x, a.x_stride = fake, (300 * 64, 1, 64)
+    a.weight, a.weight_stride = fake, (4, 1)
+    if bwd:
+        a.dout, a.dout_stride = fake, (300 * 64, 1, 64)
+        a.dx, a.dx_stride = fake, (300 * 64, 1, 64)
+        a.dweight, a.dweight_stride = fake, (4, 1)
+        a.workspace = fake
+        a.workspace_bytes = _lib.LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(a.p))
+    else:
+        a.out, a.out_stride = fake, (300 * 64, 1, 64)
+    return a
+
+
+def test_conv_validate_ok_and_errors():
+    LIB = _lib.LIB
+    assert LIB.s6_causal_conv1d_validate_fwd(ctypes.byref(conv_args())) == _lib.OK
+    assert LIB.s6_causal_conv1d_validate_bwd(ctypes.byref(conv_args(True))) == _lib.OK
+    # causal_conv1d supports widths 2..4 only
+    for w in (1, 5):
+        assert LIB.s6_causal_conv1d_validate_fwd(ctypes.byref(conv_args(width=w))) == _lib.E_UNSUPPORTED
+        assert "width" in _lib.last_error()
+    assert LIB.s6_causal_conv1d_validate_fwd(ctypes.byref(conv_args(seqlen=0))) == _lib.E_INVALID
+    assert LIB.s6_causal_conv1d_validate_fwd(ctypes.byref(conv_args(io_dtype=7))) == _lib.E_INVALID
+    a = conv_args()
+    a.out = None
+    assert LIB.s6_causal_conv1d_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "out" in _lib.last_error()
+    a = conv_args(True)
+    a.workspace_bytes -= 4
+    assert LIB.s6_causal_conv1d_validate_bwd(ctypes.byref(a)) == _lib.E_WORKSPACE
+    a = conv_args(True)
+    a.dx_stride = (300 * 64, -1, 64)
+    assert LIB.s6_causal_conv1d_validate_bwd(ctypes.byref(a)) == _lib.E_INVALID
+
+
+def test_conv_workspace_holds_one_partial_row_per_block():
+    LIB = _lib.LIB
+    small = LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(seqlen=256)))
+    assert small == 2 * 1 * 64 * 5 * 4  # one sequence block per batch row
+    big = LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(seqlen=1 << 16)))
+    assert small < big <= 2 * 256 * 64 * 5 * 4
+    assert LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(width=9))) == 0
