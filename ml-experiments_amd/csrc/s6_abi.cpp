@@ -215,7 +215,8 @@ constexpr int64_t kConvTargetBlocks = 2048;
 
 struct ConvPlan {
   int64_t T, ntile4, nsplit, tps;
-  size_t ws_bytes;
+  int64_t nslice, rps;   // first-level row slices of the partial rows
+  size_t off_ws2, ws_bytes;
 };
 
 ConvPlan conv_plan(const S6ConvProblem& p) {
@@ -228,7 +229,12 @@ ConvPlan conv_plan(const S6ConvProblem& p) {
   int64_t ns = std::min(c.ntile4, std::max<int64_t>(1, ceil_div(kConvTargetBlocks, per)));
   c.tps = ceil_div(c.ntile4, ns);
   c.nsplit = ceil_div(c.ntile4, c.tps);
-  c.ws_bytes = (size_t)(p.batch * c.nsplit * p.dim * (p.width + 1)) * 4;
+  const int64_t rows = p.batch * c.nsplit;
+  c.rps = std::max<int64_t>(32, ceil_div(rows, 64));
+  c.nslice = ceil_div(rows, c.rps);
+  const size_t row_bytes = (size_t)(p.dim * (p.width + 1)) * 4;
+  c.off_ws2 = align256(rows * row_bytes);
+  c.ws_bytes = c.off_ws2 + c.nslice * row_bytes;
   return c;
 }
 
@@ -236,6 +242,27 @@ ConvPlan conv_plan(const S6ConvProblem& p) {
 bool conv_vec_ok(const void* ptr, const int64_t s[3], int64_t vec, int es) {
   return s[1] == 1 && s[0] % vec == 0 && s[2] % vec == 0 &&
          ((uintptr_t)ptr % (uintptr_t)(vec * es)) == 0;
+}
+
+// Channels per lane: the widest vector (at most 16 bytes; 8 bytes in the backward, whose
+// per-lane state is W + 1 partial sums, a W-deep input window and a W-deep dx window per
+// channel) that every tensor's layout allows and that leaves at most 1/8 of the lanes of
+// the last channel block idle; else the allowed width that idles the fewest lanes.
+int64_t conv_pick_vec(int64_t dim, int es, bool bwd, const void* const* ptrs,
+                      const int64_t* const* strides, int n) {
+  const int64_t maxv = (bwd ? 8 : 16) / es;
+  int64_t best = 1;
+  double best_waste = 2.0;
+  for (int64_t v = maxv; v >= 1; v /= 2) {
+    bool ok = v == 1 || dim % v == 0;
+    for (int i = 0; ok && v > 1 && i < n; ++i) ok = conv_vec_ok(ptrs[i], strides[i], v, es);
+    if (!ok) continue;
+    const int64_t per = 64 * v;
+    const double waste = 1.0 - (double)dim / (double)(ceil_div(dim, per) * per);
+    if (waste <= 0.125) return v;
+    if (waste < best_waste) { best = v; best_waste = waste; }
+  }
+  return best;
 }
 
 int conv_check_problem(const S6ConvProblem& p) {
@@ -268,6 +295,7 @@ s6::ConvK conv_fill(const S6ConvProblem& p, const ConvPlan& c, int64_t vec) {
   s6::ConvK k{};
   k.Bsz = p.batch; k.D = p.dim; k.L = p.seqlen;
   k.T = c.T; k.ntile4 = c.ntile4; k.nsplit = c.nsplit; k.tps = c.tps;
+  k.nslice = c.nslice; k.rps = c.rps;
   k.nCb = ceil_div(p.dim, 64 * vec);
   return k;
 }
@@ -310,9 +338,9 @@ int s6_causal_conv1d_fwd(const S6ConvFwdArgs* a, void* stream) {
   if (r != S6_OK) return r;
   const S6ConvProblem& p = a->p;
   const int es = esize(p.io_dtype);
-  const int64_t v = 16 / es;
-  const int64_t vec = (p.dim % v == 0 && conv_vec_ok(a->x, a->x_stride, v, es) &&
-                       conv_vec_ok(a->out, a->out_stride, v, es)) ? v : 1;
+  const void* ptrs[2] = {a->x, a->out};
+  const int64_t* strides[2] = {a->x_stride, a->out_stride};
+  const int64_t vec = conv_pick_vec(p.dim, es, false, ptrs, strides, 2);
   s6::ConvK k = conv_fill(p, conv_plan(p), vec);
   for (int i = 0; i < 3; ++i) { k.sx[i] = a->x_stride[i]; k.so[i] = a->out_stride[i]; }
   k.sw[0] = a->weight_stride[0]; k.sw[1] = a->weight_stride[1]; k.sb = a->bias_stride;
@@ -328,10 +356,9 @@ int s6_causal_conv1d_bwd(const S6ConvBwdArgs* a, void* stream) {
   if (r != S6_OK) return r;
   const S6ConvProblem& p = a->p;
   const int es = esize(p.io_dtype);
-  const int64_t v = 16 / es;
-  const int64_t vec = (p.dim % v == 0 && conv_vec_ok(a->x, a->x_stride, v, es) &&
-                       conv_vec_ok(a->dout, a->dout_stride, v, es) &&
-                       conv_vec_ok(a->dx, a->dx_stride, v, es)) ? v : 1;
+  const void* ptrs[3] = {a->x, a->dout, a->dx};
+  const int64_t* strides[3] = {a->x_stride, a->dout_stride, a->dx_stride};
+  const int64_t vec = conv_pick_vec(p.dim, es, true, ptrs, strides, 3);
   s6::ConvK k = conv_fill(p, conv_plan(p), vec);
   for (int i = 0; i < 3; ++i) {
     k.sx[i] = a->x_stride[i]; k.sdo[i] = a->dout_stride[i]; k.sdx[i] = a->dx_stride[i];
@@ -339,7 +366,9 @@ int s6_causal_conv1d_bwd(const S6ConvBwdArgs* a, void* stream) {
   k.sw[0] = a->weight_stride[0]; k.sw[1] = a->weight_stride[1]; k.sb = a->bias_stride;
   k.sdw[0] = a->dweight_stride[0]; k.sdw[1] = a->dweight_stride[1]; k.sdb = a->dbias_stride;
   k.x = a->x; k.w = a->weight; k.bias = a->bias; k.dout = a->dout; k.dx = a->dx;
+  const ConvPlan c = conv_plan(p);
   k.dw = a->dweight; k.dbias = a->dbias; k.ws = (float*)a->workspace;
+  k.ws2 = (float*)((char*)a->workspace + c.off_ws2);
   hipError_t e = s6::launch_conv_bwd(k, p.io_dtype, (int)p.width, (int)vec, p.silu != 0,
                                      (hipStream_t)stream);
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_causal_conv1d_bwd: %s", hipGetErrorString(e));

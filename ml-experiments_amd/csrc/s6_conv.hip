@@ -3,9 +3,9 @@
 // (/root/reference/zoology/zoology/mixers/mamba_ssm/ops/selective_scan_interface.py:187-189,
 // 299-301).
 //
-// Work layout.  A lane owns VEC adjacent channels (VEC = 8 for 16-bit, 4 for fp32: one
-// 16-byte load per lane and step on channel-last storage; VEC = 1 for any other strides)
-// and a tile of T consecutive steps; a 256-thread block holds four waves on four adjacent
+// Work layout.  A lane owns VEC adjacent channels (VEC in 8 / 4 / 2 for channel-last
+// storage, chosen by the host so that few lanes idle: one 4- to 16-byte load per lane and
+// step; VEC = 1 for any other strides) and a tile of T consecutive steps; a 256-thread block holds four waves on four adjacent
 // tiles of the same 64*VEC channels, so the W-1 halo rows a wave re-reads were just read by
 // its neighbour.  Both kernels stream their tensors once and are HBM-bound.
 //
@@ -14,66 +14,101 @@
 // sum_k w_k dpre_{s+W-1-k} is accumulated in a second W-deep window and written when its last
 // term (t = s+W-1) arrives, so a tile of T outputs walks T+W-1 steps.  dweight / dbias are
 // summed per lane over the block's own steps, combined across the block's four waves in
-// LDS, written as one partial row per block, and reduced in fixed order by conv_reduce
-// (deterministic, no atomics).
+// LDS, written as one partial row per block, and reduced in fixed order by two conv_colsum
+// launches (deterministic, no atomics).
 #include "s6_internal.h"
 
 namespace s6 {
 namespace {
 
 constexpr int kConvWaves = 4;
+
+// 1 / (1 + e^-x) with the hardware exp2 on the rounded product -x log2(e): relative error
+// below |x| 6e-8 + 2 ulp, well inside fp32 parity for the activation's range.
+__device__ inline float conv_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
 constexpr int kConvThreads = kConvWaves * kWave;
-constexpr int kConvU = 8;     // forward: steps whose loads are issued together
+constexpr int kConvU = 8;     // forward: steps per load group (one group in flight ahead)
 constexpr int kConvUBwd = 4;  // backward (two input streams)
 
-// VEC adjacent elements at p (16-byte aligned when VEC > 1) to / from fp32.
-template <typename T, int VEC> struct VIO;
-template <typename T> struct VIO<T, 1> {
-  __device__ static inline void load(const char* p, float (&f)[1]) { f[0] = Elem<T>::load(p, 0); }
-  __device__ static inline void store(char* p, const float (&f)[1]) { Elem<T>::store(p, 0, f[0]); }
-};
-template <> struct VIO<float, 4> {
-  __device__ static inline void load(const char* p, float (&f)[4]) {
-    const float4 r = *reinterpret_cast<const float4*>(p);
-    f[0] = r.x; f[1] = r.y; f[2] = r.z; f[3] = r.w;
-  }
-  __device__ static inline void store(char* p, const float (&f)[4]) {
-    *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
-  }
-};
-template <> struct VIO<bf16, 8> {
-  __device__ static inline void load(const char* p, float (&f)[8]) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+// VEC adjacent elements at p (aligned to their total size) to / from fp32.  load_raw
+// fetches the packed bits (Raw) so that a group of loads can be in flight while the previous
+// group is computed; unpack converts them when they are used.
+template <int BYTES> struct RawOf;
+template <> struct RawOf<2> { typedef uint16_t type; };
+template <> struct RawOf<4> { typedef uint32_t type; };
+template <> struct RawOf<8> { typedef uint2 type; };
+template <> struct RawOf<16> { typedef uint4 type; };
+
+template <int NW>
+__device__ inline void words(const typename RawOf<NW * 4>::type& r, uint32_t (&w)[NW]);
+template <> __device__ inline void words<1>(const uint32_t& r, uint32_t (&w)[1]) { w[0] = r; }
+template <> __device__ inline void words<2>(const uint2& r, uint32_t (&w)[2]) { w[0] = r.x; w[1] = r.y; }
+template <> __device__ inline void words<4>(const uint4& r, uint32_t (&w)[4]) {
+  w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
+}
+template <int NW>
+__device__ inline typename RawOf<NW * 4>::type pack_words(const uint32_t (&w)[NW]);
+template <> __device__ inline uint32_t pack_words<1>(const uint32_t (&w)[1]) { return w[0]; }
+template <> __device__ inline uint2 pack_words<2>(const uint32_t (&w)[2]) { return make_uint2(w[0], w[1]); }
+template <> __device__ inline uint4 pack_words<4>(const uint32_t (&w)[4]) {
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <typename T> __device__ inline float from_bits(uint32_t h);
+template <> __device__ inline float from_bits<bf16>(uint32_t h) { return __uint_as_float(h << 16); }
+template <> __device__ inline float from_bits<f16>(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+template <typename T> __device__ inline uint32_t to_bits(float v);
+template <> __device__ inline uint32_t to_bits<bf16>(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+template <> __device__ inline uint32_t to_bits<f16>(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+template <typename T, int VEC> struct VIO {
+  static constexpr int ES = Elem<T>::kSize;
+  static constexpr int BYTES = ES * VEC;
+  typedef typename RawOf<BYTES>::type Raw;
+  __device__ static inline Raw load_raw(const char* p) { return *reinterpret_cast<const Raw*>(p); }
+  __device__ static inline void unpack(const Raw& r, float (&f)[VEC]) {
+    if constexpr (ES == 4) {
+      uint32_t w[VEC];
+      words<VEC>(r, w);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = __uint_as_float(w[i] << 16);
-      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      for (int v = 0; v < VEC; ++v) f[v] = __uint_as_float(w[v]);
+    } else if constexpr (VEC == 1) {
+      f[0] = from_bits<T>((uint32_t)r);
+    } else {
+      uint32_t w[VEC / 2];
+      words<VEC / 2>(r, w);
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) {
+        f[2 * i] = from_bits<T>(w[i] & 0xffffu);
+        f[2 * i + 1] = from_bits<T>(w[i] >> 16);
+      }
     }
   }
-  __device__ static inline void store(char* p, const float (&f)[8]) {
-    uint32_t w[4];
+  __device__ static inline void load(const char* p, float (&f)[VEC]) { unpack(load_raw(p), f); }
+  __device__ static inline void store(char* p, const float (&f)[VEC]) {
+    Raw r;
+    if constexpr (ES == 4) {
+      uint32_t w[VEC];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f[2 * i]));
-      const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f[2 * i + 1]));
-      w[i] = lo | (hi << 16);
+      for (int v = 0; v < VEC; ++v) w[v] = __float_as_uint(f[v]);
+      r = pack_words<VEC>(w);
+    } else if constexpr (VEC == 1) {
+      r = (uint16_t)to_bits<T>(f[0]);
+    } else {
+      uint32_t w[VEC / 2];
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) w[i] = to_bits<T>(f[2 * i]) | (to_bits<T>(f[2 * i + 1]) << 16);
+      r = pack_words<VEC / 2>(w);
     }
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-};
-template <> struct VIO<f16, 8> {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  __device__ static inline void load(const char* p, float (&f)[8]) {
-    const h8 r = *reinterpret_cast<const h8*>(p);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = (float)r[i];
-  }
-  __device__ static inline void store(char* p, const float (&f)[8]) {
-    h8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (_Float16)f[i];
-    *reinterpret_cast<h8*>(p) = r;
+    *reinterpret_cast<Raw*>(p) = r;
   }
 };
 
@@ -139,23 +174,31 @@ __global__ void __launch_bounds__(kConvThreads) conv_fwd(ConvK k) {
   const int64_t xs = k.sx[2] * ES, os = k.so[2] * ES;
   float win[W][VEC];
   load_halo<T, W, VEC>(xp, xs, t0, win);
+  // Group g + 1's loads are issued before group g is computed.
+  typedef typename VIO<T, VEC>::Raw Raw;
+  Raw nx[U];
+  auto issue = [&](int64_t base) {
+    const int lim = (int)min((int64_t)U, t1 - base) - 1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) nx[u] = VIO<T, VEC>::load_raw(xp + (base + min(u, lim)) * xs);
+  };
+  issue(t0);
   for (int64_t tt = t0; tt < t1; tt += U) {
     const int lim = (int)min((int64_t)U, t1 - tt) - 1;
-    const char* const xg = xp + tt * xs;
-    float cur[U][VEC];
+    Raw cx[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) VIO<T, VEC>::load(xg + min(u, lim) * xs, cur[u]);
+    for (int u = 0; u < U; ++u) cx[u] = nx[u];
+    if (tt + U < t1) issue(tt + U);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) win[W - 1][v] = cur[u][v];
+      VIO<T, VEC>::unpack(cx[u], win[W - 1]);
       float o[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
         float a = bs[v];
 #pragma unroll
         for (int j = 0; j < W; ++j) a = fmaf(wt[j][v], win[j][v], a);
-        o[v] = SILU ? a * sigmoidf_(a) : a;
+        o[v] = SILU ? a * conv_sigmoid(a) : a;
       }
       if (g.active && u <= lim) VIO<T, VEC>::store(op + (tt + u) * os, o);
 #pragma unroll
@@ -197,28 +240,42 @@ __global__ void __launch_bounds__(kConvThreads) conv_bwd(ConvK k) {
     load_halo<T, W, VEC>(xp, xs, t0, win);
 #pragma unroll
     for (int j = 0; j < W; ++j) zero<T, VEC>(acc[j]);
-    for (int64_t tt = t0; tt < te; tt += U) {
-      const int lim = (int)min((int64_t)U, te - tt) - 1;
-      float xc[U][VEC], gc[U][VEC];
+    typedef typename VIO<T, VEC>::Raw Raw;
+    Raw nx[U], ng[U];
+    auto issue = [&](int64_t base) {
+      const int lim = (int)min((int64_t)U, te - base) - 1;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        VIO<T, VEC>::load(xp + (tt + min(u, lim)) * xs, xc[u]);
-        VIO<T, VEC>::load(gp + (tt + min(u, lim)) * gs, gc[u]);
+        nx[u] = VIO<T, VEC>::load_raw(xp + (base + min(u, lim)) * xs);
+        ng[u] = VIO<T, VEC>::load_raw(gp + (base + min(u, lim)) * gs);
       }
+    };
+    issue(t0);
+    for (int64_t tt = t0; tt < te; tt += U) {
+      const int lim = (int)min((int64_t)U, te - tt) - 1;
+      Raw cx[U], cg[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        cx[u] = nx[u];
+        cg[u] = ng[u];
+      }
+      if (tt + U < te) issue(tt + U);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (u > lim) break;  // uniform
+        float gc[VEC];
+        VIO<T, VEC>::unpack(cx[u], win[W - 1]);
+        VIO<T, VEC>::unpack(cg[u], gc);
         const int64_t t = tt + u;
         const bool own = t < t1;
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
-          win[W - 1][v] = xc[u][v];
           float a = bs[v];
 #pragma unroll
           for (int j = 0; j < W; ++j) a = fmaf(wt[j][v], win[j][v], a);
-          float dp = gc[u][v];
+          float dp = gc[v];
           if (SILU) {  // d silu(a) / da = sig (1 + a (1 - sig))
-            const float sg = sigmoidf_(a);
+            const float sg = conv_sigmoid(a);
             dp *= sg * fmaf(a, 1.f - sg, 1.f);
           }
           if (own) {
@@ -274,20 +331,37 @@ __global__ void __launch_bounds__(kConvThreads) conv_bwd(ConvK k) {
   }
 }
 
-// dweight[d, j] (j < W) and dbias[d] (j == W) as the sum over the Bsz * nsplit partial rows,
-// in row order.  One thread per (d, j).
-template <int W>
-__global__ void __launch_bounds__(256) conv_reduce(ConvK k) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Column sums of the [R, n] partial matrix (n = D * (W + 1)) in two fixed-order levels:
+// block (x, y) sums rows [y * rps, min((y + 1) * rps, R)) of columns [64 x, 64 x + 64), the
+// four waves taking every fourth row and combining in LDS; the first level writes one row
+// per slice to ws2, the second (one slice) sums those rows into dweight[d, j] (j < W) and
+// dbias[d] (j == W).
+template <int W, bool FINAL>
+__global__ void __launch_bounds__(kConvThreads) conv_colsum(ConvK k, const float* src, int64_t R,
+                                                            int64_t rps, float* dst) {
+  __shared__ float red[kConvWaves - 1][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   const int64_t n = k.D * (W + 1);
-  if (i >= n) return;
-  const int64_t rows = k.Bsz * k.nsplit;
+  const int64_t col = (int64_t)blockIdx.x * kWave + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * rps, r1 = min(r0 + rps, R);
   float s = 0.f;
-  for (int64_t r = 0; r < rows; ++r) s += k.ws[r * n + i];
-  const int64_t d = i / (W + 1);
-  const int j = (int)(i % (W + 1));
-  if (j < W) k.dw[d * k.sdw[0] + j * k.sdw[1]] = s;
-  else if (k.dbias) k.dbias[d * k.sdb] = s;
+  if (col < n) {
+#pragma unroll 8
+    for (int64_t r = r0 + wv; r < r1; r += kConvWaves) s += src[r * n + col];
+  }
+  if (wv > 0) red[wv - 1][lane] = s;
+  __syncthreads();
+  if (wv != 0 || col >= n) return;
+#pragma unroll
+  for (int w = 0; w < kConvWaves - 1; ++w) s += red[w][lane];
+  if (!FINAL) {
+    dst[blockIdx.y * n + col] = s;
+  } else {
+    const int64_t d = col / (W + 1);
+    const int j = (int)(col % (W + 1));
+    if (j < W) k.dw[d * k.sdw[0] + j * k.sdw[1]] = s;
+    else if (k.dbias) k.dbias[d * k.sdb] = s;
+  }
 }
 
 template <typename T, int W, int VEC, bool SILU>
@@ -303,8 +377,14 @@ hipError_t conv_bwd_t(const ConvK& k, hipStream_t st) {
   hipLaunchKernelGGL((conv_bwd<T, W, VEC, SILU>), grid, dim3(kConvThreads), 0, st, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t n = k.D * (W + 1);
-  hipLaunchKernelGGL((conv_reduce<W>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, k);
+  const unsigned nx = (unsigned)((k.D * (W + 1) + kWave - 1) / kWave);
+  const int64_t R = k.Bsz * k.nsplit;
+  hipLaunchKernelGGL((conv_colsum<W, false>), dim3(nx, (unsigned)k.nslice), dim3(kConvThreads), 0,
+                     st, k, (const float*)k.ws, R, k.rps, k.ws2);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((conv_colsum<W, true>), dim3(nx, 1u), dim3(kConvThreads), 0, st, k,
+                     (const float*)k.ws2, k.nslice, k.nslice, (float*)nullptr);
   return hipGetLastError();
 }
 
@@ -327,16 +407,30 @@ template <bool BWD>
 hipError_t conv_dispatch(const ConvK& k, int io_dtype, int width, int vec, bool silu, hipStream_t st) {
   switch (io_dtype) {
     case S6_F32:
-      return vec == 4 ? conv_dispatch_w<BWD, float, 4>(k, width, silu, st)
-                      : conv_dispatch_w<BWD, float, 1>(k, width, silu, st);
+      switch (vec) {
+        case 4: return conv_dispatch_w<BWD, float, 4>(k, width, silu, st);
+        case 2: return conv_dispatch_w<BWD, float, 2>(k, width, silu, st);
+        case 1: return conv_dispatch_w<BWD, float, 1>(k, width, silu, st);
+      }
+      break;
     case S6_BF16:
-      return vec == 8 ? conv_dispatch_w<BWD, bf16, 8>(k, width, silu, st)
-                      : conv_dispatch_w<BWD, bf16, 1>(k, width, silu, st);
+      switch (vec) {
+        case 8: if constexpr (!BWD) return conv_dispatch_w<BWD, bf16, 8>(k, width, silu, st); break;
+        case 4: return conv_dispatch_w<BWD, bf16, 4>(k, width, silu, st);
+        case 2: return conv_dispatch_w<BWD, bf16, 2>(k, width, silu, st);
+        case 1: return conv_dispatch_w<BWD, bf16, 1>(k, width, silu, st);
+      }
+      break;
     case S6_F16:
-      return vec == 8 ? conv_dispatch_w<BWD, f16, 8>(k, width, silu, st)
-                      : conv_dispatch_w<BWD, f16, 1>(k, width, silu, st);
-    default: return hipErrorInvalidValue;
+      switch (vec) {
+        case 8: if constexpr (!BWD) return conv_dispatch_w<BWD, f16, 8>(k, width, silu, st); break;
+        case 4: return conv_dispatch_w<BWD, f16, 4>(k, width, silu, st);
+        case 2: return conv_dispatch_w<BWD, f16, 2>(k, width, silu, st);
+        case 1: return conv_dispatch_w<BWD, f16, 1>(k, width, silu, st);
+      }
+      break;
   }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace

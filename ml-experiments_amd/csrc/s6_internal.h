@@ -104,6 +104,8 @@ struct ConvK {
   const void* x; const float* w; const float* bias; void* out;
   const void* dout; void* dx; float* dw; float* dbias;
   float* ws;        // backward: [Bsz * nsplit, D, W + 1] per-block dweight | dbias partials
+  float* ws2;       // backward: [nslice, D, W + 1] sums of the partial rows per row slice
+  int64_t nslice, rps;  // backward: row slices of the partials, rows per slice
   int64_t T;        // steps per wave tile
   int64_t nCb;      // channel blocks (64 lanes x VEC channels)
   int64_t ntile4;   // blocks of 4 wave tiles along the sequence

@@ -192,8 +192,9 @@ def test_conv_validate_ok_and_errors():
 
 def test_conv_workspace_holds_one_partial_row_per_block():
     LIB = _lib.LIB
+    row = 64 * 5 * 4  # dim * (width + 1) fp32 partial sums
     small = LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(seqlen=256)))
-    assert small == 2 * 1 * 64 * 5 * 4  # one sequence block per batch row
+    assert small == 2 * row + row  # one partial row per batch row + one slice row
     big = LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(seqlen=1 << 16)))
-    assert small < big <= 2 * 256 * 64 * 5 * 4
+    assert small < big <= 2 * 256 * row + 256 + 64 * row
     assert LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(width=9))) == 0

@@ -26,17 +26,21 @@ def make_x(batch, dim, L, dtype, layout, g):
     return xg, x.mT.float()
 
 
-CONV_CASES = [  # (batch, dim, L, width, dtype, layout)
-    (2, 64, 300, 4, torch.float32, "cl"),
+CONV_CASES = [  # (batch, dim, L, width, dtype, layout); channels per lane in the comments
+    (2, 512, 300, 4, torch.bfloat16, "cl"),   # fwd 8, bwd 4
+    (2, 1024, 70, 4, torch.float16, "half"),  # fwd 8, bwd 4
+    (2, 256, 200, 3, torch.float32, "cl"),    # 4
+    (1, 768, 129, 4, torch.bfloat16, "cl"),   # 4 (8 would idle a quarter of the lanes)
+    (2, 64, 300, 4, torch.float32, "cl"),     # 1
     (2, 64, 300, 4, torch.bfloat16, "cl"),
     (2, 64, 300, 4, torch.float16, "cl"),
     (2, 64, 300, 4, torch.bfloat16, "bdl"),
-    (2, 96, 257, 3, torch.bfloat16, "half"),
+    (2, 96, 257, 3, torch.bfloat16, "half"),  # 2
     (3, 20, 130, 2, torch.bfloat16, "cl"),    # dim % 8 != 0: one channel per lane
     (3, 20, 130, 2, torch.float32, "cl"),     # dim % 4 == 0: fp32 vector path
     (1, 72, 1, 4, torch.float32, "cl"),       # seqlen 1
     (2, 16, 3, 4, torch.bfloat16, "cl"),      # seqlen < width
-    (1, 1040, 2100, 4, torch.bfloat16, "cl"),  # several channel and sequence blocks
+    (1, 1040, 2100, 4, torch.bfloat16, "cl"),  # 2; several channel and sequence blocks
 ]
 
 
