@@ -1,14 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X S6 selective scan; prints ONE JSON line on stdout.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload fwd1|fwdbwd3|fwd2|fwdbwd4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload fwd1|fwdbwd3|fwd2|fwdbwd4|mixer1|mamba3|copyref]
 
 Default workload ``fwd1``: the forward scan at B=32, L=4096, D=256, N=16, bf16 I/O with
 fp32 state (the configuration the headline metric is quoted on), called like a [B, L, D]
 producer would: ``selective_scan_fn(x.mT, delta.mT, A, B.mT, C.mT, D=D,
 return_last_state=True)``.  ``fwdbwd3`` times forward + backward at B=8, L=8192, D=768,
 N=16 bf16; ``fwd2`` the fp32 N=64 long-sequence forward; ``fwdbwd4`` the packed varlen
-forward + backward.
+forward + backward; ``mixer1`` the SSMMixer S6 core at the fwd1 shape; ``mamba3`` one
+training step of the fused Mamba block (MambaInnerFn) at the fwdbwd3 shape.
 
 * value: algorithmic HBM bytes of one step (each tensor once) / wall time per step, with
   the inputs resident in HBM.  Three independent input sets rotate so the 256 MB
@@ -46,7 +48,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="fwd1",
-                    choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "copyref"])
+                    choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "mamba3",
+                             "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -116,6 +119,144 @@ def mixer_extras(torch, inp, g):
             "dt_raw": dt_raw, "A_log": torch.log(-inp["A"])}
 
 
+MAMBA3 = dict(batch=8, seqlen=8192, d_model=384, d_state=16, d_conv=4)
+
+
+def mamba_block(torch, batch, seqlen, d_model, d_state, d_conv, dev, seed=0):
+    """Random-init parameters of a zoology Mamba layer (mamba.py:22-100: expand 2,
+    dt_rank = ceil(d_model / 16), S4D-real A, dt bias from U[1e-3, 1e-1])."""
+    d_inner = 2 * d_model
+    R = -(-d_model // 16)
+    g = torch.Generator("cpu").manual_seed(seed)
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(dev).requires_grad_(True)
+    dt = torch.exp(torch.rand(d_inner, generator=g) * (torch.log(torch.tensor(0.1))
+                                                      - torch.log(torch.tensor(1e-3)))
+                   + torch.log(torch.tensor(1e-3)))
+    return dict(
+        in_proj_weight=r(2 * d_inner, d_model, sc=d_model ** -0.5),
+        conv1d_weight=r(d_inner, 1, d_conv, sc=d_conv ** -0.5), conv1d_bias=r(d_inner, sc=0.1),
+        x_proj_weight=r(R + 2 * d_state, d_inner, sc=d_inner ** -0.5),
+        delta_proj_weight=r(d_inner, R, sc=R ** -0.5),
+        out_proj_weight=r(d_model, d_inner, sc=d_inner ** -0.5),
+        A_log=torch.log(torch.arange(1, d_state + 1, dtype=torch.float32)).repeat(d_inner, 1)
+        .to(dev).requires_grad_(True),
+        D=torch.ones(d_inner, device=dev, requires_grad=True),
+        delta_bias=(dt + torch.log(-torch.expm1(-dt))).to(dev).requires_grad_(True))
+
+
+def mamba_cpu_baseline(torch, cfg):
+    """The restated reference block (mamba_inner_ref, oracle/mamba_inner_ref.py) forward +
+    autograd backward in fp32 on the host cores, batch 1, seqlen 256 (the restated scan is
+    a Python loop over steps, about 8 s per run here)."""
+    from oracle.mamba_inner_ref import mamba_inner_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    L = 256
+    p = mamba_block(torch, 1, L, cfg["d_model"], cfg["d_state"], cfg["d_conv"], "cpu")
+    h = torch.randn(1, L, cfg["d_model"])
+
+    def run():
+        xz = (p["in_proj_weight"] @ h[0].t()).unsqueeze(0)
+        out = mamba_inner_ref(xz, p["conv1d_weight"], p["conv1d_bias"], p["x_proj_weight"],
+                              p["delta_proj_weight"], p["out_proj_weight"], None,
+                              -torch.exp(p["A_log"]), None, None, p["D"],
+                              delta_bias=p["delta_bias"], delta_softplus=True)
+        out.sum().backward()
+
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t)
+    sec = statistics.median(ts)
+    d_inner = 2 * cfg["d_model"]
+    return {"value": round(L * d_inner / sec / 1e6, 4), "unit": "Mtok·ch/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"restated reference block (mamba_inner_ref: nn.Conv1d path, "
+                       f"selective_scan_ref op for op, autograd backward), fp32, batch 1, "
+                       f"seqlen {L}, d_model {cfg['d_model']}; median of 3 runs = {sec:.3f} s")}
+
+
+def run_mamba(torch, args):
+    """Workload mamba3: one training step (forward + backward) of the fused Mamba block
+    (s6scan.mamba_inner.mamba_inner_fn, the reference's MambaInnerFn path, mamba.py:138-153)
+    under bf16 autocast: in_proj, HIP causal conv1d + SiLU, x_proj / dt_proj GEMMs, HIP
+    selective scan (softplus, D, z gate), out_proj, and the backward of all of it."""
+    from s6scan import mamba_inner
+    c = MAMBA3
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, L, dm, N = c["batch"], c["seqlen"], c["d_model"], c["d_state"]
+    d_inner = 2 * dm
+    sets = []
+    for s in range(2):  # two rotating input sets
+        g = torch.Generator("cpu").manual_seed(100 + s)
+        sets.append((torch.randn(B, L, dm, generator=g).to(dev, torch.bfloat16),
+                     torch.randn(B, L, dm, generator=g).to(dev, torch.bfloat16)))
+    p = mamba_block(torch, B, L, dm, N, c["d_conv"], dev)
+
+    def step(i):
+        h, dy = sets[i % len(sets)]
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            xz = torch.nn.functional.linear(h, p["in_proj_weight"]).mT
+            out = mamba_inner.mamba_inner_fn(
+                xz, p["conv1d_weight"], p["conv1d_bias"], p["x_proj_weight"],
+                p["delta_proj_weight"], p["out_proj_weight"], None, -torch.exp(p["A_log"]),
+                None, None, p["D"], delta_bias=p["delta_bias"], delta_softplus=True)
+        out.backward(dy)
+        for t in p.values():
+            t.grad = None
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    K = args.steps
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    evs = [(mk(), mk()) for _ in range(K)]
+    stream = torch.cuda.current_stream()
+    for pair in evs:
+        for e in pair:
+            e.record(stream)
+    g0, g1 = mk(), mk()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g0.record(stream)
+    for i in range(K):
+        mamba_inner.KERNEL_EVENTS = evs[i]
+        step(i)
+    g1.record(stream)
+    torch.cuda.synchronize()
+    mamba_inner.KERNEL_EVENTS = None
+    ms_step = (time.perf_counter() - t0) * 1e3 / K
+    kb_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    # bwd_scan algorithmic bytes (each tensor once): u, delta, dout, z, out read and du,
+    # ddelta, dz, out_z written (bf16); B, C read (bf16) and dB, dC written (fp32); A, D,
+    # delta_bias in and their gradients out (fp32).
+    E = B * L * d_inner
+    kb_bytes = E * 2 * 9 + B * L * N * (2 + 2 + 4 + 4) + 2 * (4 * d_inner * N + 8 * d_inner)
+    achieved = kb_bytes / (kb_ms * 1e-3) / 1e9
+    res = {
+        "metric": "fused Mamba block (MambaInnerFn) fwd+bwd Mtok·ch/s at 1 GPU",
+        "value": round(B * L * d_inner / (ms_step * 1e-3) / 1e6, 2),
+        "unit": "Mtok·ch/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal hidden states and output gradients; random-init "
+                "parameters of a zoology Mamba layer)",
+        "config": {"workload": (f"mamba3: zoology Mamba fast path, batch {B}, seqlen {L}, "
+                                f"d_model {dm}, d_inner {d_inner}, d_state {N}, d_conv "
+                                f"{c['d_conv']}, bf16 autocast, fwd+bwd")},
+        "gpu_event_ms_per_step": round(g0.elapsed_time(g1) / K, 5),
+        "roofline": {"kernel": "bwd_scan (softplus, z gate, out_z recompute)", "bound": "hbm",
+                     "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "kernel_ms": round(kb_ms, 5)},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        res["cpu_baseline"] = mamba_cpu_baseline(torch, c)
+    print(json.dumps(res), flush=True)
+
+
 def copy_reference(torch, steps):
     """Plain device-to-device copy of a known size (1 GiB read + 1 GiB written per launch).
     Profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between those
@@ -144,6 +285,9 @@ def main():
         copy_reference(torch, args.steps)
         return
     import s6scan
+    if args.workload == "mamba3":
+        run_mamba(torch, args)
+        return
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
 

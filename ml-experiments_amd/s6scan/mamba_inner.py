@@ -34,6 +34,11 @@ from .causal_conv1d import causal_conv1d_bwd, causal_conv1d_fwd
 from .selective_scan_interface import selective_scan_backward, selective_scan_forward
 
 
+# Measurement hook: a pair of already-recorded torch.cuda.Events, re-recorded by the library
+# around the backward scan kernel of every MambaInnerFn.backward while it is set (None: off).
+KERNEL_EVENTS = None
+
+
 def _channel_last(t):
     """[batch, C, L] -> the same values with stride(1) == 1 (no copy when already so)."""
     return t if t.stride(1) == 1 else t.mT.contiguous().mT
@@ -126,7 +131,7 @@ class MambaInnerFn(torch.autograd.Function):
         dout_y = _as_bcl(dout @ out_proj_weight, batch, L)  # (batch, d_inner, seqlen)
         (dconv1d_out, ddelta, dA, dB, dC, dD, _, ddelta_bias, out_z) = selective_scan_backward(
             conv1d_out, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout_y, x_ckpt,
-            out=out, dz_out=dz, recompute_out_z=True)
+            out=out, dz_out=dz, recompute_out_z=True, kernel_events=KERNEL_EVENTS)
         dout_proj_weight = dout.t() @ _flat(out_z)
         dout_proj_bias = dout.sum(dim=0) if not ctx.out_proj_bias_is_None else None
         dD = dD if D is not None else None
