@@ -2,7 +2,7 @@
 """Benchmark of the MI355X S6 selective scan; prints ONE JSON line on stdout.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload fwd1|fwdbwd3|fwd2|fwdbwd4|mixer1|mamba3|copyref]
+                    [--workload fwd1|fwdbwd3|fwd2|fwdbwd4|mixer1|mamba3|decode|copyref]
 
 Default workload ``fwd1``: the forward scan at B=32, L=4096, D=256, N=16, bf16 I/O with
 fp32 state (the configuration the headline metric is quoted on), called like a [B, L, D]
@@ -10,7 +10,8 @@ producer would: ``selective_scan_fn(x.mT, delta.mT, A, B.mT, C.mT, D=D,
 return_last_state=True)``.  ``fwdbwd3`` times forward + backward at B=8, L=8192, D=768,
 N=16 bf16; ``fwd2`` the fp32 N=64 long-sequence forward; ``fwdbwd4`` the packed varlen
 forward + backward; ``mixer1`` the SSMMixer S6 core at the fwd1 shape; ``mamba3`` one
-training step of the fused Mamba block (MambaInnerFn) at the fwdbwd3 shape.
+training step of the fused Mamba block (MambaInnerFn) at the fwdbwd3 shape; ``decode`` the
+selective_state_update decode step (batch 64, d_inner 1536), graph-launched.
 
 * value: algorithmic HBM bytes of one step (each tensor once) / wall time per step, with
   the inputs resident in HBM.  Three independent input sets rotate so the 256 MB
@@ -49,7 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="fwd1",
                     choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "mamba3",
-                             "copyref"])
+                             "decode", "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -257,6 +258,94 @@ def run_mamba(torch, args):
     print(json.dumps(res), flush=True)
 
 
+DECODE = dict(batch=64, dim=1536, dstate=16, steps_per_graph=16)
+
+
+def run_decode(torch, args):
+    """Workload decode: the recurrent decode step (s6scan.selective_state_update, the
+    reference's selective_state_update, selective_state_update.py:121-201) of a Mamba layer
+    with d_inner 1536 for 64 sequences: fp32 state updated in place, bf16 x / dt / z / B / C,
+    softplus(dt + dt_bias), D and the z gate.  16 consecutive steps (each with its own inputs)
+    are captured in one HIP graph, as a serving loop runs them, and the graph is replayed."""
+    from s6scan.selective_state_update import selective_state_update
+    c = DECODE
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, D, N, S = c["batch"], c["dim"], c["dstate"], c["steps_per_graph"]
+    g = torch.Generator("cpu").manual_seed(5)
+    r = lambda *sh, dt=torch.float32: torch.randn(*sh, generator=g).to(dev, dt)
+    bf = torch.bfloat16
+    state = r(B, D, N)
+    A = -torch.exp(r(D, N))
+    Dp, bias = r(D), 0.2 * r(D)
+    steps = [dict(x=r(B, D, dt=bf), dt=(0.5 * r(B, D) - 1.0).to(bf), z=r(B, D, dt=bf),
+                  B=r(B, N, dt=bf), C=r(B, N, dt=bf)) for _ in range(S)]
+
+    def run_steps():
+        return [selective_state_update(state, s_["x"], s_["dt"], A, s_["B"], s_["C"], Dp,
+                                       s_["z"], bias, True) for s_ in steps]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_steps()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_steps()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    K = args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(K):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_step = (time.perf_counter() - t0) * 1e6 / (K * S)
+    ev_us = e0.elapsed_time(e1) * 1e3 / (K * S)
+    # bytes per step, each tensor once: state read + written (fp32), A (fp32), x, dt, z, out
+    # (bf16), B, C (bf16), D, dt_bias (fp32)
+    nbytes = B * D * N * 4 * 2 + D * N * 4 + 4 * B * D * 2 + 2 * B * N * 2 + 2 * D * 4
+    achieved = nbytes / (ev_us * 1e-6) / 1e9
+    res = {
+        "metric": "selective_state_update decode step latency (us per step) at 1 GPU",
+        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": K * S,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded normal inputs)",
+        "config": {"workload": (f"decode: selective_state_update, batch {B}, dim {D}, dstate "
+                                f"{N}, fp32 state, bf16 x/dt/z/B/C, softplus + dt_bias + D + z; "
+                                f"{S} steps per HIP graph")},
+        "gpu_event_us_per_step": round(ev_us, 3),
+        "roofline": {"kernel": "ssu_rows_kernel (one per step, graph-launched)", "bound": "hbm",
+                     "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "kernel_us_incl_graph_gaps": round(ev_us, 3)},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        from oracle.selective_state_update_ref import selective_state_update_ref
+        torch.set_num_threads(os.cpu_count() or 1)
+        st = state.cpu()
+        cs = [{k: v.cpu() for k, v in s_.items()} for s_ in steps]
+        Ac, Dc, bc = A.cpu(), Dp.cpu(), bias.cpu()
+        ts = []
+        for _ in range(3):
+            t = time.perf_counter()
+            for s_ in cs:
+                selective_state_update_ref(st, s_["x"], s_["dt"], Ac, s_["B"], s_["C"], Dc,
+                                           s_["z"], bc, True)
+            ts.append((time.perf_counter() - t) * 1e6 / S)
+        res["cpu_baseline"] = {"value": round(statistics.median(ts), 3), "unit": "us/step",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"restated selective_state_update_ref, the full "
+                                         f"workload ({S} steps, median of 3 runs)"}
+    print(json.dumps(res), flush=True)
+
+
 def copy_reference(torch, steps):
     """Plain device-to-device copy of a known size (1 GiB read + 1 GiB written per launch).
     Profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between those
@@ -287,6 +376,9 @@ def main():
     import s6scan
     if args.workload == "mamba3":
         run_mamba(torch, args)
+        return
+    if args.workload == "decode":
+        run_decode(torch, args)
         return
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward

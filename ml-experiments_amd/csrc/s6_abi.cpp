@@ -8,6 +8,7 @@
 #include <string>
 
 #include "s6_internal.h"
+#include "selective_state_update.h"
 
 namespace {
 
@@ -300,9 +301,85 @@ s6::ConvK conv_fill(const S6ConvProblem& p, const ConvPlan& c, int64_t vec) {
   return k;
 }
 
+int ssu_check(const S6StateUpdateArgs& a) {
+  int r;
+  if (a.batch < 1 || a.nheads < 1 || a.dim < 1 || a.dstate < 1 || a.ngroups < 1)
+    return fail(S6_E_INVALID, "selective_state_update: batch, nheads, dim, dstate, ngroups must be >= 1");
+  if (a.nheads % a.ngroups != 0)
+    return fail(S6_E_INVALID, "selective_state_update: nheads must be divisible by ngroups");
+  if (a.dstate > S6_SSU_MAX_DSTATE)
+    return fail(S6_E_UNSUPPORTED, "selective_state_update: dstate must be <= %d, got %lld",
+                S6_SSU_MAX_DSTATE, (long long)a.dstate);
+  if (a.batch > 65535 || a.nheads > 65535 || ceil_div(a.dim, 64) > ((int64_t)1 << 31) - 1)
+    return fail(S6_E_UNSUPPORTED, "selective_state_update: batch / nheads / dim too large");
+  for (int dt : {a.state_dtype, a.io_dtype, a.bc_dtype})
+    if (dt != S6_F32 && dt != S6_BF16 && dt != S6_F16)
+      return fail(S6_E_INVALID, "selective_state_update: bad dtype %d", dt);
+  if ((r = check_ptr(a.state, "state")) || (r = check_strides(a.state_stride, 4, "state")) ||
+      (r = check_ptr(a.x, "x")) || (r = check_strides(a.x_stride, 3, "x")) ||
+      (r = check_ptr(a.dt, "dt")) || (r = check_strides(a.dt_stride, 3, "dt")) ||
+      (r = check_ptr(a.A, "A")) || (r = check_strides(a.A_stride, 3, "A")) ||
+      (r = check_ptr(a.B, "B")) || (r = check_strides(a.B_stride, 3, "B")) ||
+      (r = check_ptr(a.C, "C")) || (r = check_strides(a.C_stride, 3, "C")) ||
+      (r = check_ptr(a.out, "out")) || (r = check_strides(a.out_stride, 3, "out")))
+    return r;
+  if (a.has_D && ((r = check_ptr(a.D, "D")) || (r = check_strides(a.D_stride, 2, "D")))) return r;
+  if (a.has_z && ((r = check_ptr(a.z, "z")) || (r = check_strides(a.z_stride, 3, "z")))) return r;
+  if (a.has_dt_bias &&
+      ((r = check_ptr(a.dt_bias, "dt_bias")) || (r = check_strides(a.dt_bias_stride, 2, "dt_bias"))))
+    return r;
+  return S6_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int s6_validate_state_update(const S6StateUpdateArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  int r = ssu_check(*a);
+  return r != S6_OK ? r : ok();
+}
+
+int s6_selective_state_update(const S6StateUpdateArgs* a, void* stream) {
+  int r = s6_validate_state_update(a);
+  if (r != S6_OK) return r;
+  s6::SsuK k{};
+  k.batch = a->batch; k.nheads = a->nheads; k.dim = a->dim; k.dstate = a->dstate;
+  k.hpg = a->nheads / a->ngroups;
+  k.io = a->io_dtype; k.bc = a->bc_dtype;
+  k.state = a->state; k.x = a->x; k.dt = a->dt; k.A = a->A; k.B = a->B; k.C = a->C;
+  k.out = a->out;
+  k.bias = a->has_dt_bias ? a->dt_bias : nullptr;
+  k.Dp = a->has_D ? a->D : nullptr;
+  k.z = a->has_z ? a->z : nullptr;
+  for (int i = 0; i < 4; ++i) k.ss[i] = a->state_stride[i];
+  for (int i = 0; i < 3; ++i) {
+    k.sx[i] = a->x_stride[i]; k.sdt[i] = a->dt_stride[i]; k.sA[i] = a->A_stride[i];
+    k.sB[i] = a->B_stride[i]; k.sC[i] = a->C_stride[i]; k.so[i] = a->out_stride[i];
+    k.sz[i] = a->has_z ? a->z_stride[i] : 0;
+  }
+  for (int i = 0; i < 2; ++i) {
+    k.sbias[i] = a->has_dt_bias ? a->dt_bias_stride[i] : 0;
+    k.sD[i] = a->has_D ? a->D_stride[i] : 0;
+  }
+  // Row mapping: 4 contiguous states per lane in one 16-byte (fp32) or 8-byte load; A and
+  // B / C rows vector-loaded when their layout allows it.
+  auto rows4 = [](const void* p, const int64_t* st, int n, int es) {
+    if (st[n - 1] != 1 || (uintptr_t)p % (uintptr_t)(4 * es) != 0) return false;
+    for (int i = 0; i < n - 1; ++i)
+      if (st[i] % 4 != 0) return false;
+    return true;
+  };
+  const bool rows = a->dstate % 4 == 0 && rows4(a->state, a->state_stride, 4, esize(a->state_dtype));
+  k.a_vec = rows4(a->A, a->A_stride, 3, 4);
+  k.bc_vec = rows4(a->B, a->B_stride, 3, esize(a->bc_dtype)) &&
+             rows4(a->C, a->C_stride, 3, esize(a->bc_dtype));
+  hipError_t e = s6::launch_state_update(k, a->state_dtype, a->dt_softplus != 0, rows,
+                                         (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_selective_state_update: %s", hipGetErrorString(e));
+  return ok();
+}
 
 int s6_causal_conv1d_validate_fwd(const S6ConvFwdArgs* a) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");

@@ -113,6 +113,23 @@ struct ConvK {
   int64_t tps;      // backward: tile blocks per split
 };
 
+// Parameter block of the selective_state_update kernel (strides in elements).
+struct SsuK {
+  int64_t batch, nheads, dim, dstate, hpg;   // hpg: heads per B / C group
+  int32_t io, bc;                            // dtypes of x / dt / z / out and of B / C
+  void* state; int64_t ss[4];
+  const void* x; int64_t sx[3];
+  const void* dt; int64_t sdt[3];
+  const float* bias; int64_t sbias[2];       // NULL: no dt_bias
+  const float* A; int64_t sA[3];
+  const void* B; int64_t sB[3];
+  const void* C; int64_t sC[3];
+  const float* Dp; int64_t sD[2];            // NULL: no D
+  const void* z; int64_t sz[3];              // NULL: no z
+  void* out; int64_t so[3];
+  int32_t a_vec, bc_vec;   // row kernel: A / B and C rows contiguous and 4-element aligned
+};
+
 inline hipError_t record_event(void* const* ev, int i, hipStream_t st) {
   if (ev == nullptr || ev[i] == nullptr) return hipSuccess;
   return hipEventRecord((hipEvent_t)ev[i], st);
@@ -137,6 +154,10 @@ hipError_t launch_conv_fwd(const ConvK& k, int io_dtype, int width, int vec, boo
                            hipStream_t st);
 hipError_t launch_conv_bwd(const ConvK& k, int io_dtype, int width, int vec, bool silu,
                            hipStream_t st);
+// s6_ssu.hip: one decode step of the state.
+// rows: the state and A rows are contiguous and 16-byte aligned (vectorised row mapping).
+hipError_t launch_state_update(const SsuK& k, int state_dtype, bool softplus, bool rows,
+                               hipStream_t st);
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
 hipError_t launch_relayout(const void* src, const int64_t s[4], int esize, void* dst,
                            int64_t Bsz, int64_t G, int64_t N, int64_t NP, int64_t L,

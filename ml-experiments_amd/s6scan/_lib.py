@@ -1,4 +1,5 @@
-"""ctypes binding of the s6scan C ABI (``include/s6scan.h``, ``include/causal_conv1d.h``).
+"""ctypes binding of the s6scan C ABI (``include/s6scan.h``, ``include/causal_conv1d.h``,
+``include/selective_state_update.h``).
 
 The shared library is built in-tree (``ml-experiments_amd/build.py``) next to this file.
 There is no fallback: if the library is missing or was built for another ABI version,
@@ -121,6 +122,24 @@ class S6ConvBwdArgs(ctypes.Structure):
     ]
 
 
+class S6StateUpdateArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("dim", _i64), ("dstate", _i64), ("ngroups", _i64),
+        ("state_dtype", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
+        ("has_D", _i32), ("has_z", _i32), ("has_dt_bias", _i32), ("dt_softplus", _i32),
+        ("state", _vp), ("state_stride", _a(4)),
+        ("x", _vp), ("x_stride", _a(3)),
+        ("dt", _vp), ("dt_stride", _a(3)),
+        ("dt_bias", _vp), ("dt_bias_stride", _a(2)),
+        ("A", _vp), ("A_stride", _a(3)),
+        ("B", _vp), ("B_stride", _a(3)),
+        ("C", _vp), ("C_stride", _a(3)),
+        ("D", _vp), ("D_stride", _a(2)),
+        ("z", _vp), ("z_stride", _a(3)),
+        ("out", _vp), ("out_stride", _a(3)),
+    ]
+
+
 EXPORTS = {
     "s6_abi_version": (ctypes.c_int, []),
     "s6_last_error": (ctypes.c_char_p, []),
@@ -137,6 +156,8 @@ EXPORTS = {
     "s6_causal_conv1d_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6ConvProblem)]),
     "s6_causal_conv1d_fwd": (ctypes.c_int, [ctypes.POINTER(S6ConvFwdArgs), ctypes.c_void_p]),
     "s6_causal_conv1d_bwd": (ctypes.c_int, [ctypes.POINTER(S6ConvBwdArgs), ctypes.c_void_p]),
+    "s6_validate_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs)]),
+    "s6_selective_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs), ctypes.c_void_p]),
 }
 
 
