@@ -9,6 +9,7 @@
 
 #include "s6_internal.h"
 #include "selective_state_update.h"
+#include "ssd.h"
 
 namespace {
 
@@ -331,9 +332,136 @@ int ssu_check(const S6StateUpdateArgs& a) {
   return S6_OK;
 }
 
+// ---- Mamba-2 SSD ------------------------------------------------------------------------
+
+struct SsdPlan {
+  int64_t K;
+  size_t off_dtq, off_dacs, off_st, off_hs, off_cb, total;
+};
+
+SsdPlan ssd_plan(const S6SsdProblem& p) {
+  SsdPlan s{};
+  s.K = ceil_div(p.seqlen, p.chunk_size);
+  const size_t bhkq = (size_t)(p.batch * p.nheads * s.K * p.chunk_size) * 4;
+  const size_t pn = (size_t)(p.batch * s.K * p.nheads * p.headdim * p.dstate);
+  size_t off = 0;
+  s.off_dtq = off; off += align256(bhkq);
+  s.off_dacs = off; off += align256(bhkq);
+  s.off_st = off; off += align256(pn * 4);
+  s.off_hs = off; off += align256(pn * (size_t)esize(p.io_dtype));
+  s.off_cb = off; off += align256((size_t)(p.batch * s.K * p.ngroups) * p.chunk_size * p.chunk_size * 4);
+  s.total = off;
+  return s;
+}
+
+int ssd_check_problem(const S6SsdProblem& p) {
+  if (p.batch < 1 || p.seqlen < 1 || p.nheads < 1 || p.ngroups < 1)
+    return fail(S6_E_INVALID, "ssd: batch, seqlen, nheads, ngroups must be >= 1");
+  if (p.nheads % p.ngroups != 0)
+    return fail(S6_E_INVALID, "ssd: nheads must be divisible by ngroups");
+  if (p.headdim != 32 && p.headdim != 64 && p.headdim != 128)
+    return fail(S6_E_UNSUPPORTED, "ssd: headdim must be 32, 64 or 128, got %lld", (long long)p.headdim);
+  if (p.dstate != 32 && p.dstate != 64 && p.dstate != 128 && p.dstate != 256)
+    return fail(S6_E_UNSUPPORTED, "ssd: dstate must be 32, 64, 128 or 256, got %lld", (long long)p.dstate);
+  if (p.chunk_size != 64 && p.chunk_size != 128 && p.chunk_size != 256)
+    return fail(S6_E_UNSUPPORTED, "ssd: chunk_size must be 64, 128 or 256, got %lld",
+                (long long)p.chunk_size);
+  if (p.io_dtype != S6_BF16 && p.io_dtype != S6_F32)
+    return fail(S6_E_UNSUPPORTED, "ssd: io dtype must be bf16 or fp32");
+  if (ceil_div(p.seqlen, p.chunk_size) > 65535 || p.batch * p.nheads > 65535 || p.batch > 65535)
+    return fail(S6_E_UNSUPPORTED, "ssd: too many chunks or batch * nheads above 65535");
+  if (!(p.dt_min <= p.dt_max)) return fail(S6_E_INVALID, "ssd: dt_limit must satisfy min <= max");
+  return S6_OK;
+}
+
+// Rows read with 16-byte vector loads: unit stride along the last axis and 16-byte aligned
+// row starts.
+int ssd_check_rows(const void* ptr, const int64_t* s, int es, const char* name) {
+  if (s[3] != 1) return fail(S6_E_INVALID, "ssd: %s must have unit stride along its last axis", name);
+  if ((uintptr_t)ptr % 16 != 0 || (s[0] * es) % 16 != 0 || (s[1] * es) % 16 != 0 ||
+      (s[2] * es) % 16 != 0)
+    return fail(S6_E_INVALID, "ssd: %s rows must start on 16-byte boundaries", name);
+  return S6_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int s6_ssd_validate_fwd(const S6SsdFwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  const S6SsdProblem& p = a->p;
+  int r;
+  if ((r = ssd_check_problem(p))) return r;
+  const int es = esize(p.io_dtype);
+  if ((r = check_ptr(a->x, "x")) || (r = check_strides(a->x_stride, 4, "x")) ||
+      (r = ssd_check_rows(a->x, a->x_stride, es, "x")) ||
+      (r = check_ptr(a->dt, "dt")) || (r = check_strides(a->dt_stride, 3, "dt")) ||
+      (r = check_ptr(a->A, "A")) || (r = check_ptr(a->B, "B")) ||
+      (r = check_strides(a->B_stride, 4, "B")) || (r = ssd_check_rows(a->B, a->B_stride, es, "B")) ||
+      (r = check_ptr(a->C, "C")) || (r = check_strides(a->C_stride, 4, "C")) ||
+      (r = ssd_check_rows(a->C, a->C_stride, es, "C")) ||
+      (r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out")))
+    return r;
+  if (a->A_stride < 0) return fail(S6_E_INVALID, "A has a negative stride");
+  if (p.has_D && ((r = check_ptr(a->D, "D")) || (r = check_strides(a->D_stride, 2, "D")))) return r;
+  if (p.has_z && ((r = check_ptr(a->z, "z")) || (r = check_strides(a->z_stride, 4, "z")))) return r;
+  if (p.has_z && a->out_x && (r = check_strides(a->out_x_stride, 4, "out_x"))) return r;
+  if (p.has_dt_bias && (r = check_ptr(a->dt_bias, "dt_bias"))) return r;
+  if (p.has_initial_states && ((r = check_ptr(a->initial_states, "initial_states")) ||
+                               (r = check_strides(a->initial_states_stride, 4, "initial_states"))))
+    return r;
+  if (p.has_seq_idx && ((r = check_ptr(a->seq_idx, "seq_idx")) ||
+                        (r = check_strides(a->seq_idx_stride, 2, "seq_idx"))))
+    return r;
+  const SsdPlan pl = ssd_plan(p);
+  if (a->workspace == nullptr || a->workspace_bytes < pl.total)
+    return fail(S6_E_WORKSPACE, "ssd forward workspace needs %zu bytes, got %zu", pl.total,
+                a->workspace ? a->workspace_bytes : (size_t)0);
+  return ok();
+}
+
+size_t s6_ssd_fwd_workspace_bytes(const S6SsdProblem* p) {
+  if (p == nullptr || ssd_check_problem(*p) != S6_OK) return 0;
+  return ssd_plan(*p).total;
+}
+
+int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream) {
+  int r = s6_ssd_validate_fwd(a);
+  if (r != S6_OK) return r;
+  const S6SsdProblem& p = a->p;
+  const SsdPlan pl = ssd_plan(p);
+  s6::SsdK k{};
+  k.Bsz = p.batch; k.L = p.seqlen; k.H = p.nheads; k.P = p.headdim; k.G = p.ngroups;
+  k.N = p.dstate; k.Q = p.chunk_size; k.K = pl.K; k.hpg = p.nheads / p.ngroups;
+  k.io = p.io_dtype;
+  k.softplus = p.dt_softplus; k.has_bias = p.has_dt_bias; k.has_D = p.has_D;
+  k.D_hdim = p.D_has_hdim; k.has_z = p.has_z; k.has_init = p.has_initial_states;
+  k.has_seq = p.has_seq_idx; k.dt_min = p.dt_min; k.dt_max = p.dt_max;
+  k.x = a->x; k.dt = a->dt; k.A = a->A; k.sA = a->A_stride; k.Bm = a->B; k.Cm = a->C;
+  k.Dp = p.has_D ? a->D : nullptr; k.z = p.has_z ? a->z : nullptr;
+  k.bias = p.has_dt_bias ? a->dt_bias : nullptr; k.sbias = a->dt_bias_stride;
+  k.init = p.has_initial_states ? a->initial_states : nullptr;
+  k.seq = p.has_seq_idx ? a->seq_idx : nullptr;
+  k.out = a->out; k.out_x = p.has_z ? a->out_x : nullptr; k.final_states = a->final_states;
+  for (int i = 0; i < 4; ++i) {
+    k.sx[i] = a->x_stride[i]; k.sB[i] = a->B_stride[i]; k.sC[i] = a->C_stride[i];
+    k.sz[i] = p.has_z ? a->z_stride[i] : 0; k.sout[i] = a->out_stride[i];
+    k.soutx[i] = (p.has_z && a->out_x) ? a->out_x_stride[i] : 0;
+    k.sinit[i] = p.has_initial_states ? a->initial_states_stride[i] : 0;
+  }
+  for (int i = 0; i < 3; ++i) k.sdt[i] = a->dt_stride[i];
+  for (int i = 0; i < 2; ++i) {
+    k.sD[i] = p.has_D ? a->D_stride[i] : 0;
+    k.sseq[i] = p.has_seq_idx ? a->seq_idx_stride[i] : 0;
+  }
+  char* ws = (char*)a->workspace;
+  k.dtq = (float*)(ws + pl.off_dtq); k.dacs = (float*)(ws + pl.off_dacs);
+  k.st = (float*)(ws + pl.off_st); k.hs = ws + pl.off_hs; k.cb = (float*)(ws + pl.off_cb);
+  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_fwd: %s", hipGetErrorString(e));
+  return ok();
+}
 
 int s6_validate_state_update(const S6StateUpdateArgs* a) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");

@@ -113,6 +113,46 @@ struct ConvK {
   int64_t tps;      // backward: tile blocks per split
 };
 
+// Loads / stores of one element whose dtype is a wave-uniform runtime value.
+__device__ inline float load_any(const void* p, int64_t i, int dt) {
+  if (dt == S6_F32) return Elem<float>::load(p, i);
+  if (dt == S6_BF16) return Elem<bf16>::load(p, i);
+  return Elem<f16>::load(p, i);
+}
+
+__device__ inline void store_any(void* p, int64_t i, float v, int dt) {
+  if (dt == S6_F32) Elem<float>::store(p, i, v);
+  else if (dt == S6_BF16) Elem<bf16>::store(p, i, v);
+  else Elem<f16>::store(p, i, v);
+}
+
+// Parameter block of the Mamba-2 SSD kernels (strides in elements).
+struct SsdK {
+  int64_t Bsz, L, H, P, G, N, Q, K;   // K = number of chunks of Q steps
+  int64_t hpg;                        // heads per B / C group
+  int32_t io;                         // dtype of x, z, B, C, dt, out
+  int32_t softplus, has_bias, has_D, D_hdim, has_z, has_init, has_seq;
+  float dt_min, dt_max;
+  const void* x; int64_t sx[4];
+  const void* dt; int64_t sdt[3];
+  const float* A; int64_t sA;
+  const void* Bm; int64_t sB[4];
+  const void* Cm; int64_t sC[4];
+  const float* Dp; int64_t sD[2];
+  const void* z; int64_t sz[4];
+  const float* bias; int64_t sbias;
+  const float* init; int64_t sinit[4];
+  const int32_t* seq; int64_t sseq[2];
+  void* out; int64_t sout[4];
+  void* out_x; int64_t soutx[4];      // NULL: not written
+  float* final_states;                // NULL: not written
+  float* dtq;   // [Bsz, H, K, Q] processed dt (0 past the sequence end)
+  float* dacs;  // [Bsz, H, K, Q] cumulative dt * A within each chunk
+  float* st;    // [Bsz, K, H, P, N] chunk states
+  void* hs;     // [Bsz, K, H, P, N] state entering each chunk (io dtype)
+  float* cb;    // [Bsz, K, G, Q, Q] C B^T within each chunk (lower-triangle tiles written)
+};
+
 // Parameter block of the selective_state_update kernel (strides in elements).
 struct SsuK {
   int64_t batch, nheads, dim, dstate, hpg;   // hpg: heads per B / C group
@@ -154,6 +194,8 @@ hipError_t launch_conv_fwd(const ConvK& k, int io_dtype, int width, int vec, boo
                            hipStream_t st);
 hipError_t launch_conv_bwd(const ConvK& k, int io_dtype, int width, int vec, bool silu,
                            hipStream_t st);
+// s6_ssd.hip: the Mamba-2 SSD forward.
+hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st);
 // s6_ssu.hip: one decode step of the state.
 // rows: the state and A rows are contiguous and 16-byte aligned (vectorised row mapping).
 hipError_t launch_state_update(const SsuK& k, int state_dtype, bool softplus, bool rows,

@@ -1,0 +1,458 @@
+// Mamba-2 SSD forward (chunked scan with scalar A per head), the computation of
+// _mamba_chunk_scan_combined_fwd (/root/reference/zoology/zoology/mixers/mamba_ssm/ops/
+// triton/ssd_combined.py:281-332), in five kernels:
+//
+//   ssd_cumsum        dt -> dt' = clamp(softplus(dt + bias)), S = cumsum(dt' A) per chunk
+//                     (ssd_chunk_state.py:34-84 semantics)
+//   ssd_chunk_state   st_c[p, n] = sum_l x_l[p] (dt'_l e^{S_last - S_l}) B_l[n]     MFMA
+//                     (ssd_chunk_state.py:177-266)
+//   ssd_state_pass    H_{c+1} = e^{S_last,c} H_c + st_c, reset across seq_idx changes
+//                     (ssd_state_passing.py:28-91)
+//   ssd_bmm           CB_c[l, s] = C_l . B_s within each chunk, lower triangle        MFMA
+//                     (ssd_bmm.py:35-106)
+//   ssd_chunk_scan    y_l = e^{S_l} C_l H_c^T + sum_{s<=l} CB[l,s] e^{S_l-S_s} dt'_s x_s
+//                     + D x_l, then * silu(z)                                       MFMA
+//                     (ssd_chunk_scan.py:43-185)
+//
+// MFMA use.  Every contraction runs on 16x16 output tiles with K = 32 per step: one
+// v_mfma_f32_16x16x32_bf16 for bf16 operands, eight v_mfma_f32_16x16x4_f32 for fp32.
+// Lane i of a wave holds A[i % 16][k(i, j)] and B[k(i, j)][i % 16] for items j < 8, with
+// k(i, j) = 8 (i / 16) + j (bf16) or i / 16 + 4 j (fp32), and D[4 (i / 16) + j][i % 16]
+// for j < 4.  Operands whose K axis is the sequence (x and B in the chunk state, x in the
+// chunk scan) are staged through LDS transposed, so each lane's 8 K-items are one 16-byte
+// LDS read; operands whose K axis is dstate (C, B in CB; C and the passed states in the
+// scan) are read straight from global memory, 16 bytes per lane.
+//
+// Precision follows the reference's rounding points: the scaled B of the chunk state and
+// the decayed CB of the chunk scan are rounded to the input type before the MFMA, the
+// passed states are stored in the input type, chunk states, CB and all accumulation are
+// fp32.
+#include "s6_internal.h"
+#include "ssd.h"
+
+namespace s6 {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr int kKs = 32;            // sequence steps per MFMA K step (and per LDS slice)
+constexpr int kLp = kKs + 8;       // LDS row pitch in elements: 16-byte aligned rows
+constexpr int kThreads = 256;
+
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+  typedef __bf16 Frag __attribute__((ext_vector_type(8)));
+  typedef uint16_t Raw;
+  static constexpr int kVe = 8;  // elements per 16-byte load
+  __device__ static inline int kidx(int lane, int j) { return 8 * (lane >> 4) + j; }
+  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
+    return *reinterpret_cast<const Frag*>(row_k0 + 8 * (lane >> 4));
+  }
+  __device__ static inline Frag from_float(const float (&v)[8]) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);
+    return f;
+  }
+  __device__ static inline Frag zero() {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(0.f);
+    return f;
+  }
+  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  __device__ static inline Raw to_raw(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  }
+  __device__ static inline float from_raw(Raw r) { return __uint_as_float((uint32_t)r << 16); }
+};
+template <> struct Mma<float> {
+  struct Frag { float v[8]; };
+  typedef float Raw;
+  static constexpr int kVe = 4;
+  __device__ static inline int kidx(int lane, int j) { return (lane >> 4) + 4 * j; }
+  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = row_k0[(lane >> 4) + 4 * j];
+    return f;
+  }
+  __device__ static inline Frag from_float(const float (&v)[8]) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = v[j];
+    return f;
+  }
+  __device__ static inline Frag zero() {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = 0.f;
+    return f;
+  }
+  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
+  }
+  __device__ static inline Raw to_raw(float v) { return v; }
+  __device__ static inline float from_raw(Raw r) { return r; }
+};
+
+// 16 bytes of a row, as kVe raw elements.
+template <typename T>
+__device__ inline void load16(const void* p, typename Mma<T>::Raw (&r)[Mma<T>::kVe]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  *reinterpret_cast<uint4*>(r) = v;
+}
+
+__device__ inline int32_t seq_at(const SsdK& k, int64_t b, int64_t t) {
+  return k.seq[b * k.sseq[0] + t * k.sseq[1]];
+}
+
+// ---- 1. dt processing and per-chunk cumulative decay ---------------------------------
+
+__global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
+  const int64_t hh = (int64_t)blockIdx.x * kWave + threadIdx.x;
+  if (hh >= k.H) return;
+  const int64_t c = blockIdx.y, b = blockIdx.z;
+  const float A = k.A[hh * k.sA];
+  const float bias = k.has_bias ? k.bias[hh * k.sbias] : 0.f;
+  const int64_t row = ((b * k.H + hh) * k.K + c) * k.Q;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  float acc = 0.f;
+  for (int l = 0; l < (int)k.Q; ++l) {
+    float v = 0.f;
+    if (l < lim) {
+      v = load_any(k.dt, b * k.sdt[0] + (t0 + l) * k.sdt[1] + hh * k.sdt[2], k.io) + bias;
+      if (k.softplus) v = softplus20(v);
+      v = fminf(fmaxf(v, k.dt_min), k.dt_max);
+    }
+    acc += v * A;
+    k.dtq[row + l] = v;
+    k.dacs[row + l] = acc;
+  }
+}
+
+// ---- 2. chunk states -----------------------------------------------------------------
+
+template <typename T, int P, int N>
+__global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  constexpr int VE = M::kVe;
+  constexpr int NTN = N / 16;
+  constexpr int NT = (P / 16) * NTN;
+  constexpr int TPW = (NT + 3) / 4;
+  __shared__ __attribute__((aligned(16))) Raw xs[P][kLp];
+  __shared__ __attribute__((aligned(16))) Raw bs[N][kLp];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t c = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int64_t g = hh / k.hpg;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  const float* sq = k.dacs + ((b * k.H + hh) * k.K + c) * k.Q;
+  const float* dq = k.dtq + ((b * k.H + hh) * k.K + c) * k.Q;
+  const float s_last = sq[k.Q - 1];
+  const int32_t seq_last = k.has_seq ? seq_at(k, b, t0 + lim - 1) : 0;
+  constexpr int ES = sizeof(Raw);
+  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
+  const char* bbase = (const char*)k.Bm + (b * k.sB[0] + t0 * k.sB[1] + g * k.sB[2]) * ES;
+
+  f4 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int l0 = 0; l0 < lim; l0 += kKs) {
+    // x rows l0..l0+31 -> xs[p][l]; zero past the sequence end
+    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      Raw v[VE];
+      if (l0 + r < lim) load16<T>(xbase + ((l0 + r) * k.sx[1] + col) * ES, v);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) xs[col + q][r] = v[q];
+    }
+    // B rows scaled by dt'_l e^{S_last - S_l} (0 outside the last sequence) -> bs[n][l]
+    for (int e = tid; e < kKs * (N / VE); e += kThreads) {
+      const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+      const int l = l0 + r;
+      float wl = 0.f;
+      Raw v[VE];
+      if (l < lim) {
+        load16<T>(bbase + (l * k.sB[1] + col) * ES, v);
+        wl = dq[l] * exp_split(s_last - sq[l]);
+        if (k.has_seq && seq_at(k, b, t0 + l) != seq_last) wl = 0.f;
+      } else {
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+      }
+#pragma unroll
+      for (int q = 0; q < VE; ++q) bs[col + q][r] = M::to_raw(M::from_raw(v[q]) * wl);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int ti = w + 4 * i;
+      if (ti < NT) {
+        const int pt = ti / NTN, nt = ti % NTN;
+        const typename M::Frag a = M::load_row(&xs[pt * 16 + (lane & 15)][0], lane);
+        const typename M::Frag bf = M::load_row(&bs[nt * 16 + (lane & 15)][0], lane);
+        M::mma(acc[i], a, bf);
+      }
+    }
+    __syncthreads();
+  }
+  float* out = k.st + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int ti = w + 4 * i;
+    if (ti < NT) {
+      const int pt = ti / NTN, nt = ti % NTN;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        out[(pt * 16 + 4 * (lane >> 4) + j) * N + nt * 16 + (lane & 15)] = acc[i][j];
+    }
+  }
+}
+
+// ---- 3. state passing across chunks --------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) ssd_state_pass(SsdK k) {
+  typedef typename Mma<T>::Raw Raw;
+  const int64_t PN = k.P * k.N;
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= PN) return;
+  const int64_t hh = blockIdx.y, b = blockIdx.z;
+  const int64_t p = e / k.N, n = e % k.N;
+  float H = k.has_init ? k.init[b * k.sinit[0] + hh * k.sinit[1] + p * k.sinit[2] + n * k.sinit[3]] : 0.f;
+  int32_t seq_prev = 0;
+  Raw* hs = (Raw*)k.hs;
+  for (int64_t c = 0; c < k.K; ++c) {
+    const int64_t o = ((b * k.K + c) * k.H + hh) * PN + e;
+    hs[o] = Mma<T>::to_raw(H);
+    float scale = exp_split(k.dacs[((b * k.H + hh) * k.K + c) * k.Q + k.Q - 1]);
+    if (k.has_seq) {
+      const int32_t sn = seq_at(k, b, min((c + 1) * k.Q, k.L) - 1);
+      if (sn != seq_prev) scale = 0.f;
+      seq_prev = sn;
+    }
+    H = scale * H + k.st[o];
+  }
+  if (k.final_states) k.final_states[(b * k.H + hh) * PN + e] = H;
+}
+
+// ---- 4. C B^T within each chunk ------------------------------------------------------
+
+template <typename T, int N>
+__global__ void __launch_bounds__(kThreads) ssd_bmm(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int ti = 0, rem = (int)blockIdx.x;  // lower-triangle 64x64 tile (ti, tj), tj <= ti
+  while (rem > ti) { rem -= ti + 1; ++ti; }
+  const int tj = rem;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  const Raw* Cb = (const Raw*)k.Cm + b * k.sC[0] + t0 * k.sC[1] + g * k.sC[2];
+  const Raw* Bb = (const Raw*)k.Bm + b * k.sB[0] + t0 * k.sB[1] + g * k.sB[2];
+  const int row = ti * 64 + 16 * w + (lane & 15);
+  f4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int n0 = 0; n0 < N; n0 += kKs) {
+    const typename M::Frag a = row < lim ? M::load_row(Cb + row * k.sC[1] + n0, lane) : M::zero();
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int s = tj * 64 + 16 * ct + (lane & 15);
+      const typename M::Frag bf = s < lim ? M::load_row(Bb + s * k.sB[1] + n0, lane) : M::zero();
+      M::mma(acc[ct], a, bf);
+    }
+  }
+  float* out = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = ti * 64 + 16 * w + 4 * (lane >> 4) + j;
+      const int s = tj * 64 + 16 * ct + (lane & 15);
+      float v = acc[ct][j];
+      if (k.has_seq && l < lim && s < lim && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
+      out[(int64_t)l * k.Q + s] = v;
+    }
+  }
+}
+
+// ---- 5. chunk scan -------------------------------------------------------------------
+
+template <typename T, int P, int N>
+__global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  constexpr int VE = M::kVe;
+  constexpr int PT = P / 16;
+  constexpr int ES = sizeof(Raw);
+  __shared__ __attribute__((aligned(16))) Raw xs[P][kLp];
+  __shared__ float sls[kKs], dls[kKs];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lt = blockIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.H, hh = blockIdx.z % k.H;
+  const int64_t g = hh / k.hpg;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  if (lt * 64 >= lim) return;  // whole block
+  const float* sq = k.dacs + ((b * k.H + hh) * k.K + c) * k.Q;
+  const float* dq = k.dtq + ((b * k.H + hh) * k.K + c) * k.Q;
+  const int rowbase = lt * 64 + 16 * w;
+  const int row = rowbase + (lane & 15);  // A-operand row of this lane
+  f4 acc[PT];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // (a) contribution of the state entering the chunk: e^{S_l} C_l H_c^T
+  if (c > 0 || k.has_init) {
+    const Raw* Crow = (const Raw*)k.Cm + b * k.sC[0] + (t0 + row) * k.sC[1] + g * k.sC[2];
+    const Raw* H = (const Raw*)k.hs + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+#pragma unroll
+    for (int n0 = 0; n0 < N; n0 += kKs) {
+      const typename M::Frag a = row < lim ? M::load_row(Crow + n0, lane) : M::zero();
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt)
+        M::mma(acc[pt], a, M::load_row(H + (pt * 16 + (lane & 15)) * N + n0, lane));
+    }
+    const int32_t seq_prev = (k.has_seq && c > 0) ? seq_at(k, b, t0 - 1) : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      float f = 0.f;
+      if (l < lim) {
+        f = exp_split(sq[l]);
+        if (k.has_seq && seq_at(k, b, t0 + l) != seq_prev) f = 0.f;
+      }
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt) acc[pt][j] *= f;
+    }
+  }
+
+  // (b) within the chunk: sum_{s <= l} CB[l, s] e^{S_l - S_s} dt'_s x_s
+  const float s_row = row < lim ? sq[row] : 0.f;
+  const float* cbrow = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + (int64_t)row * k.Q;
+  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
+  const int s_end = min(lt * 64 + 64, lim);
+  for (int s0 = 0; s0 < s_end; s0 += kKs) {
+    __syncthreads();  // the previous slice is consumed
+    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      Raw v[VE];
+      if (s0 + r < lim) load16<T>(xbase + ((s0 + r) * k.sx[1] + col) * ES, v);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) xs[col + q][r] = v[q];
+    }
+    if (tid < kKs) {
+      sls[tid] = sq[s0 + tid];
+      dls[tid] = dq[s0 + tid];
+    }
+    __syncthreads();
+    if (s0 <= rowbase + 15) {  // wave-uniform: the slice reaches this wave's rows
+      float m[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int si = M::kidx(lane, j);
+        const int s = s0 + si;
+        const float cbv = cbrow[s];
+        const bool on = s <= row && row < lim && s < lim;
+        const float v = cbv * exp_split(s_row - sls[si]) * dls[si];
+        m[j] = on ? v : 0.f;
+      }
+      const typename M::Frag a = M::from_float(m);
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt)
+        M::mma(acc[pt], a, M::load_row(&xs[pt * 16 + (lane & 15)][0], lane));
+    }
+  }
+
+  // (c) D skip, z gate, stores
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = rowbase + 4 * (lane >> 4) + j;
+    if (l >= lim) continue;
+    const int64_t t = t0 + l;
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      const int p = pt * 16 + (lane & 15);
+      float y = acc[pt][j];
+      if (k.has_D) {
+        const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + p * k.sD[1]] : k.Dp[hh * k.sD[0]];
+        y = fmaf(Dv, Elem<T>::load(k.x, b * k.sx[0] + t * k.sx[1] + hh * k.sx[2] + p), y);
+      }
+      if (k.has_z) {
+        if (k.out_x) Elem<T>::store(k.out_x, b * k.soutx[0] + t * k.soutx[1] + hh * k.soutx[2] + p, y);
+        const float zz = Elem<T>::load(k.z, b * k.sz[0] + t * k.sz[1] + hh * k.sz[2] + p);
+        y *= zz * sigmoidf_(zz);
+      }
+      Elem<T>::store(k.out, b * k.sout[0] + t * k.sout[1] + hh * k.sout[2] + p, y);
+    }
+  }
+}
+
+// ---- dispatch ------------------------------------------------------------------------
+
+template <typename T, int P, int N>
+hipError_t ssd_fwd_pn(const SsdK& k, hipStream_t st) {
+  hipError_t e;
+  hipLaunchKernelGGL((ssd_cumsum), dim3((unsigned)((k.H + kWave - 1) / kWave), (unsigned)k.K,
+                     (unsigned)k.Bsz), dim3(kWave), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
+                     dim3(kThreads), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_state_pass<T>), dim3((unsigned)((P * N + kThreads - 1) / kThreads),
+                     (unsigned)k.H, (unsigned)k.Bsz), dim3(kThreads), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int qt = (int)(k.Q / 64);
+  hipLaunchKernelGGL((ssd_bmm<T, N>), dim3((unsigned)(qt * (qt + 1) / 2), (unsigned)k.K,
+                     (unsigned)(k.Bsz * k.G)), dim3(kThreads), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_chunk_scan<T, P, N>), dim3((unsigned)qt, (unsigned)k.K,
+                     (unsigned)(k.Bsz * k.H)), dim3(kThreads), 0, st, k);
+  return hipGetLastError();
+}
+
+template <typename T, int P>
+hipError_t ssd_fwd_p(const SsdK& k, hipStream_t st) {
+  switch (k.N) {
+    case 32: return ssd_fwd_pn<T, P, 32>(k, st);
+    case 64: return ssd_fwd_pn<T, P, 64>(k, st);
+    case 128: return ssd_fwd_pn<T, P, 128>(k, st);
+    case 256: return ssd_fwd_pn<T, P, 256>(k, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T>
+hipError_t ssd_fwd_t(const SsdK& k, hipStream_t st) {
+  switch (k.P) {
+    case 32: return ssd_fwd_p<T, 32>(k, st);
+    case 64: return ssd_fwd_p<T, 64>(k, st);
+    case 128: return ssd_fwd_p<T, 128>(k, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st) {
+  if (k.io == S6_BF16) return ssd_fwd_t<bf16>(k, st);
+  if (k.io == S6_F32) return ssd_fwd_t<float>(k, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace s6

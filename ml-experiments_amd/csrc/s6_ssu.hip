@@ -18,18 +18,7 @@ namespace s6 {
 namespace {
 
 // The state's storage type is a template parameter; the row tensors' and B / C's dtypes are
-// wave-uniform runtime switches (one or two elements per lane and group).
-__device__ inline float load_any(const void* p, int64_t i, int dt) {
-  if (dt == S6_F32) return Elem<float>::load(p, i);
-  if (dt == S6_BF16) return Elem<bf16>::load(p, i);
-  return Elem<f16>::load(p, i);
-}
-
-__device__ inline void store_any(void* p, int64_t i, float v, int dt) {
-  if (dt == S6_F32) Elem<float>::store(p, i, v);
-  else if (dt == S6_BF16) Elem<bf16>::store(p, i, v);
-  else Elem<f16>::store(p, i, v);
-}
+// wave-uniform runtime switches (load_any / store_any, one or two elements per lane).
 
 constexpr int kSsuGroup = 16;
 

@@ -1,5 +1,5 @@
 """ctypes binding of the s6scan C ABI (``include/s6scan.h``, ``include/causal_conv1d.h``,
-``include/selective_state_update.h``).
+``include/selective_state_update.h``, ``include/ssd.h``).
 
 The shared library is built in-tree (``ml-experiments_amd/build.py``) next to this file.
 There is no fallback: if the library is missing or was built for another ABI version,
@@ -140,6 +140,34 @@ class S6StateUpdateArgs(ctypes.Structure):
     ]
 
 
+class S6SsdProblem(ctypes.Structure):
+    _fields_ = [("batch", _i64), ("seqlen", _i64), ("nheads", _i64), ("headdim", _i64),
+                ("ngroups", _i64), ("dstate", _i64), ("chunk_size", _i64),
+                ("io_dtype", _i32), ("has_D", _i32), ("D_has_hdim", _i32), ("has_z", _i32),
+                ("has_dt_bias", _i32), ("dt_softplus", _i32), ("has_initial_states", _i32),
+                ("has_seq_idx", _i32), ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float)]
+
+
+class S6SsdFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("p", S6SsdProblem),
+        ("x", _vp), ("x_stride", _a(4)),
+        ("dt", _vp), ("dt_stride", _a(3)),
+        ("A", _vp), ("A_stride", _i64),
+        ("B", _vp), ("B_stride", _a(4)),
+        ("C", _vp), ("C_stride", _a(4)),
+        ("D", _vp), ("D_stride", _a(2)),
+        ("z", _vp), ("z_stride", _a(4)),
+        ("dt_bias", _vp), ("dt_bias_stride", _i64),
+        ("initial_states", _vp), ("initial_states_stride", _a(4)),
+        ("seq_idx", _vp), ("seq_idx_stride", _a(2)),
+        ("out", _vp), ("out_stride", _a(4)),
+        ("out_x", _vp), ("out_x_stride", _a(4)),
+        ("final_states", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 EXPORTS = {
     "s6_abi_version": (ctypes.c_int, []),
     "s6_last_error": (ctypes.c_char_p, []),
@@ -156,6 +184,9 @@ EXPORTS = {
     "s6_causal_conv1d_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6ConvProblem)]),
     "s6_causal_conv1d_fwd": (ctypes.c_int, [ctypes.POINTER(S6ConvFwdArgs), ctypes.c_void_p]),
     "s6_causal_conv1d_bwd": (ctypes.c_int, [ctypes.POINTER(S6ConvBwdArgs), ctypes.c_void_p]),
+    "s6_ssd_validate_fwd": (ctypes.c_int, [ctypes.POINTER(S6SsdFwdArgs)]),
+    "s6_ssd_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6SsdProblem)]),
+    "s6_ssd_fwd": (ctypes.c_int, [ctypes.POINTER(S6SsdFwdArgs), ctypes.c_void_p]),
     "s6_validate_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs)]),
     "s6_selective_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs), ctypes.c_void_p]),
 }

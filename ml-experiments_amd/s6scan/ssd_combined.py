@@ -1,0 +1,133 @@
+"""Mamba-2 SSD (``mamba_chunk_scan_combined``) on the gfx950 kernels of ``libs6scan.so``.
+
+Same signature, argument meaning and return values as the reference's
+``mamba_chunk_scan_combined`` (/root/reference/zoology/zoology/mixers/mamba_ssm/ops/triton/
+ssd_combined.py:563-582, forward :281-332):
+
+    mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                              initial_states=None, seq_idx=None, cu_seqlens=None,
+                              dt_softplus=False, dt_limit=(0.0, inf),
+                              return_final_states=False, return_varlen_states=False)
+        -> out | (out, final_states)
+
+* x, z: (batch, seqlen, nheads, headdim); dt: (batch, seqlen, nheads); A, dt_bias:
+  (nheads,); B, C: (batch, seqlen, ngroups, dstate); D: (nheads,) or (nheads, headdim);
+  initial_states: (batch, nheads, headdim, dstate); seq_idx: (batch, seqlen) int32.
+* out has x's dtype (bf16 or fp32); final_states is fp32 (batch, nheads, headdim, dstate).
+
+The forward runs five HIP kernels (chunk cumsum, chunk states and C B^T on MFMA, state
+passing, the chunk scan on MFMA); see ml-experiments_amd/csrc/s6_ssd.hip.  Supported
+shapes: headdim 32 / 64 / 128, dstate 32 / 64 / 128 / 256, chunk_size 64 / 128 / 256.
+There is no CPU path.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _st(t, n):
+    return tuple(t.stride()) if t is not None else (0,) * n
+
+
+def _rows16(t):
+    """t with unit last stride and 16-byte aligned rows (a contiguous copy otherwise), as
+    the reference makes B / C / x contiguous when their last stride is not 1
+    (ssd_combined.py:297-304)."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all((s * es) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initial_states=None,
+                seq_idx=None, dt_softplus=False, dt_limit=(0.0, float("inf")),
+                want_final_states=False, want_out_x=False):
+    """One forward launch sequence.  Returns (out, out_x, final_states); out_x (the output
+    before the z gate) only with z and ``want_out_x``, final_states only when asked."""
+    batch, seqlen, nheads, headdim = x.shape
+    _, _, ngroups, dstate = B.shape
+    assert nheads % ngroups == 0
+    assert B.shape == (batch, seqlen, ngroups, dstate)
+    assert dt.shape == (batch, seqlen, nheads)
+    assert A.shape == (nheads,)
+    assert C.shape == B.shape
+    if z is not None:
+        assert z.shape == x.shape
+    if D is not None:
+        assert D.shape == (nheads, headdim) or D.shape == (nheads,)
+    if seq_idx is not None:
+        assert seq_idx.shape == (batch, seqlen)
+    if initial_states is not None:
+        assert initial_states.shape == (batch, nheads, headdim, dstate)
+    if not x.is_cuda:
+        raise RuntimeError("mamba_chunk_scan_combined: tensors must be on a ROCm device (no CPU path)")
+    if x.dtype not in _DTYPES:
+        raise NotImplementedError(f"mamba_chunk_scan_combined: dtype {x.dtype} (bf16 or fp32 only)")
+    dtype = x.dtype
+    B, C = B.to(dtype), C.to(dtype)
+    x, B, C = _rows16(x), _rows16(B), _rows16(C)
+    if z is not None:
+        z = _rows16(z.to(dtype))
+    dt = dt.to(dtype)
+    f32 = lambda t: None if t is None else t.float()
+    A, D, dt_bias, initial_states = f32(A), f32(D), f32(dt_bias), f32(initial_states)
+    if seq_idx is not None:
+        seq_idx = seq_idx.to(torch.int32)
+    with torch.cuda.device(x.device):
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+        out_x = torch.empty_like(out) if (z is not None and want_out_x) else None
+        final = (torch.empty(batch, nheads, headdim, dstate, dtype=torch.float32, device=x.device)
+                 if want_final_states else None)
+        a = _lib.S6SsdFwdArgs()
+        a.p = _lib.S6SsdProblem(batch, seqlen, nheads, headdim, ngroups, dstate, chunk_size,
+                                _DTYPES[dtype], int(D is not None),
+                                int(D is not None and D.dim() == 2), int(z is not None),
+                                int(dt_bias is not None), int(bool(dt_softplus)),
+                                int(initial_states is not None), int(seq_idx is not None),
+                                float(dt_limit[0]), float(dt_limit[1]))
+        a.x, a.x_stride = _ptr(x), _st(x, 4)
+        a.dt, a.dt_stride = _ptr(dt), _st(dt, 3)
+        a.A, a.A_stride = _ptr(A), A.stride(0)
+        a.B, a.B_stride = _ptr(B), _st(B, 4)
+        a.C, a.C_stride = _ptr(C), _st(C, 4)
+        Dm = None if D is None else (D if D.dim() == 2 else D[:, None])
+        a.D, a.D_stride = _ptr(Dm), _st(Dm, 2)
+        a.z, a.z_stride = _ptr(z), _st(z, 4)
+        a.dt_bias = _ptr(dt_bias)
+        a.dt_bias_stride = dt_bias.stride(0) if dt_bias is not None else 0
+        a.initial_states, a.initial_states_stride = _ptr(initial_states), _st(initial_states, 4)
+        a.seq_idx, a.seq_idx_stride = _ptr(seq_idx), _st(seq_idx, 2)
+        a.out, a.out_stride = _ptr(out), _st(out, 4)
+        a.out_x, a.out_x_stride = _ptr(out_x), _st(out_x, 4)
+        a.final_states = _ptr(final)
+        nbytes = _lib.LIB.s6_ssd_fwd_workspace_bytes(ctypes.byref(a.p))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        a.workspace, a.workspace_bytes = _ptr(ws), nbytes
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(_lib.LIB.s6_ssd_fwd(ctypes.byref(a), ctypes.c_void_p(stream)), "s6_ssd_fwd")
+    return out, out_x, final
+
+
+def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                              initial_states=None, seq_idx=None, cu_seqlens=None,
+                              dt_softplus=False, dt_limit=(0.0, float("inf")),
+                              return_final_states=False, return_varlen_states=False):
+    if cu_seqlens is not None or return_varlen_states:
+        raise NotImplementedError("mamba_chunk_scan_combined: varlen states are not built yet")
+    if any(t is not None and t.requires_grad for t in (x, dt, A, B, C, D, z, dt_bias,
+                                                       initial_states)) and torch.is_grad_enabled():
+        raise NotImplementedError("mamba_chunk_scan_combined: the backward is not built yet")
+    out, _, final = ssd_forward(x, dt, A, B, C, chunk_size, D=D, z=z, dt_bias=dt_bias,
+                                initial_states=initial_states, seq_idx=seq_idx,
+                                dt_softplus=dt_softplus, dt_limit=dt_limit,
+                                want_final_states=return_final_states)
+    return out if not return_final_states else (out, final)

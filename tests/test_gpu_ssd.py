@@ -1,0 +1,108 @@
+"""GPU parity of the Mamba-2 SSD forward (s6scan.ssd_combined) against the CPU restatement of
+the reference's chunked pipeline (oracle/ssd_ref.py, pinned by its float64 brute force),
+computed in float64 on the same (16-bit-rounded) inputs."""
+import pytest
+import torch
+
+import s6scan  # noqa: F401
+from oracle.ssd_ref import ssd_chunked_ref
+from s6scan.ssd_combined import mamba_chunk_scan_combined, ssd_forward
+from tolerances import assert_close, rms
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make(batch, L, H, P, G, N, dtype, seed, opts=()):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g)
+    t = dict(x=r(batch, L, H, P).to(dtype), dt=(0.5 * r(batch, L, H) - 1.0).to(dtype),
+             A=-torch.exp(torch.rand(H, generator=g) * 2.77),  # A in [-16, -1] as Mamba-2's init
+             B=r(batch, L, G, N).to(dtype), C=r(batch, L, G, N).to(dtype))
+    kw = dict(dt_softplus=True)
+    if "D" in opts:
+        t["D"] = r(H)
+    if "D_hdim" in opts:
+        t["D"] = r(H, P)
+    if "z" in opts:
+        t["z"] = r(batch, L, H, P).to(dtype)
+    if "bias" in opts:
+        t["dt_bias"] = 0.5 * r(H)
+    if "init" in opts:
+        t["initial_states"] = r(batch, H, P, N)
+    if "seq" in opts:
+        seq = torch.zeros(batch, L, dtype=torch.int32)
+        for b in range(batch):
+            cuts = sorted(torch.randint(1, L, (3,), generator=g).tolist())
+            for i, cpos in enumerate(cuts):
+                seq[b, cpos:] = i + 1
+        t["seq_idx"] = seq
+    if "limit" in opts:
+        kw["dt_limit"] = (0.05, 0.5)
+    return t, kw
+
+
+def check(out, ref, dtype, what):
+    if dtype == torch.float32:
+        assert_close(out, ref, 1e-4, 1e-4 * rms(ref), what)
+    else:  # the scaled B, the decayed CB and the passed states are rounded to bf16 (as in the
+        # reference); compare norm-wise and elementwise against the float64 value
+        d = (out.float().cpu() - ref.float())
+        rel = (d.norm() / ref.float().norm()).item()
+        assert rel < 1.5e-2, f"{what}: norm-wise relative error {rel:.3g}"
+        assert_close(out, ref, 5e-2, 5e-2 * rms(ref), what)
+
+
+CASES = [  # batch, L, H, P, G, N, chunk, opts
+    (2, 300, 4, 64, 2, 64, 64, ("D", "z", "bias")),
+    (1, 512, 2, 32, 1, 128, 128, ("init", "seq", "D")),
+    (2, 256, 3, 128, 3, 32, 256, ("D_hdim", "limit", "bias")),
+    (1, 1000, 2, 64, 1, 256, 256, ("z", "init")),
+    (2, 190, 8, 64, 1, 128, 64, ("seq", "init", "z", "D", "bias")),
+    (1, 64, 1, 32, 1, 32, 64, ()),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", CASES)
+def test_ssd_forward_matches_reference(case, dtype):
+    batch, L, H, P, G, N, Q, opts = case
+    t, kw = make(batch, L, H, P, G, N, dtype, seed=L + N, opts=opts)
+    gpu = {k: v.to(DEV) for k, v in t.items()}
+    out, out_x, final = ssd_forward(**gpu, chunk_size=Q, want_final_states=True,
+                                    want_out_x=True, **kw)
+    ref, ref_x, ref_final = ssd_chunked_ref(**t, chunk_size=Q, compute_dtype=torch.float64, **kw)
+    assert out.shape == (batch, L, H, P) and out.dtype == dtype
+    check(out, ref, dtype, "out")
+    if "z" in opts:
+        check(out_x, ref_x, dtype, "out_x")
+    check(final, ref_final, torch.float32 if dtype == torch.float32 else dtype, "final_states")
+
+
+def test_ssd_mamba2_defaults_bf16():
+    """Mamba-2's default layer: headdim 64, dstate 128, chunk 256, one group, D per head,
+    dt bias + softplus, no z (the RMSNorm variant); x, B, C are views of one xBC buffer."""
+    batch, L, H, P, N = 2, 1024, 8, 64, 128
+    g = torch.Generator().manual_seed(17)
+    xBC = torch.randn(batch, L, H * P + 2 * N, generator=g).to(torch.bfloat16)
+    x = xBC[..., :H * P].reshape(batch, L, H, P)
+    B = xBC[..., H * P:H * P + N].reshape(batch, L, 1, N)
+    C = xBC[..., H * P + N:].reshape(batch, L, 1, N)
+    dt = (0.5 * torch.randn(batch, L, H, generator=g) - 2.0).to(torch.bfloat16)
+    A = -torch.exp(torch.rand(H, generator=g) * 2.77)
+    D, bias = torch.randn(H, generator=g), 0.3 * torch.randn(H, generator=g)
+    dv = lambda v: v.to(DEV)
+    xg = dv(xBC)
+    out = mamba_chunk_scan_combined(
+        xg[..., :H * P].reshape(batch, L, H, P), dv(dt), dv(A),
+        xg[..., H * P:H * P + N].reshape(batch, L, 1, N), xg[..., H * P + N:].reshape(batch, L, 1, N),
+        256, D=dv(D), dt_bias=dv(bias), dt_softplus=True)
+    ref, _, _ = ssd_chunked_ref(x, dt, A, B, C, 256, D=D, dt_bias=bias, dt_softplus=True,
+                                compute_dtype=torch.float64)
+    check(out, ref, torch.bfloat16, "out")
+
+
+def test_ssd_rejects_unsupported_shapes():
+    t, kw = make(1, 64, 1, 48, 1, 32, torch.float32, seed=1)
+    with pytest.raises(RuntimeError, match="headdim"):
+        ssd_forward(**{k: v.to(DEV) for k, v in t.items()}, chunk_size=64, **kw)
