@@ -63,11 +63,45 @@ typedef struct S6SsdFwdArgs {
   void* workspace;             size_t workspace_bytes;
 } S6SsdFwdArgs;
 
+typedef struct S6SsdBwdArgs {
+  S6SsdProblem p;
+  const void* x;               int64_t x_stride[4];
+  const void* dt;              int64_t dt_stride[3];
+  const float* A;              int64_t A_stride;
+  const void* B;               int64_t B_stride[4];
+  const void* C;               int64_t C_stride[4];
+  const float* D;              int64_t D_stride[2];
+  const void* z;               int64_t z_stride[4];
+  const float* dt_bias;        int64_t dt_bias_stride;
+  const float* initial_states; int64_t initial_states_stride[4];
+  const int32_t* seq_idx;      int64_t seq_idx_stride[2];
+  const void* dout;            int64_t dout_stride[4];   /* headdim stride 1, 16-byte rows */
+  const void* out_x;           int64_t out_x_stride[4];  /* forward y before the z gate; has_z */
+  const float* dfinal_states;  int64_t dfinal_states_stride[4];  /* NULL = zero */
+  void* dx;                    int64_t dx_stride[4];
+  void* ddt;                   int64_t ddt_stride[3];
+  float* dA;                   /* [nheads] */
+  void* dB;                    int64_t dB_stride[4];
+  void* dC;                    int64_t dC_stride[4];
+  float* dD;                   /* [nheads] or [nheads, headdim] contiguous; has_D */
+  void* dz;                    int64_t dz_stride[4];     /* has_z */
+  float* ddt_bias;             /* [nheads]; has_dt_bias */
+  float* dinitial_states;      /* [batch, nheads, headdim, dstate] contiguous; NULL = not written */
+  void* workspace;             size_t workspace_bytes;
+} S6SsdBwdArgs;
+
 int s6_ssd_validate_fwd(const S6SsdFwdArgs* a);
 size_t s6_ssd_fwd_workspace_bytes(const S6SsdProblem* p);
 
 /* Replaces _mamba_chunk_scan_combined_fwd (ssd_combined.py:281-332). */
 int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream);
+
+int s6_ssd_validate_bwd(const S6SsdBwdArgs* a);
+size_t s6_ssd_bwd_workspace_bytes(const S6SsdProblem* p);
+
+/* Replaces _mamba_chunk_scan_combined_bwd (ssd_combined.py:335-452): writes dx, ddt, dA, dB,
+ * dC and, when present, dD, dz, ddt_bias, dinitial_states (overwritten, deterministic). */
+int s6_ssd_bwd(const S6SsdBwdArgs* a, void* stream);
 
 #ifdef __cplusplus
 }

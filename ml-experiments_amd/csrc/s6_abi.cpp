@@ -337,6 +337,10 @@ int ssu_check(const S6StateUpdateArgs& a) {
 struct SsdPlan {
   int64_t K;
   size_t off_dtq, off_dacs, off_st, off_hs, off_cb, total;
+  // backward
+  int64_t nE;
+  size_t off_dyw, off_dst, off_ddal, off_ddtd, off_dDp, off_qv, off_uv, off_rs, off_csp;
+  size_t off_dBp, off_dCp, off_dcb, off_dAp, off_dbp, total_bwd;
 };
 
 SsdPlan ssd_plan(const S6SsdProblem& p) {
@@ -351,6 +355,24 @@ SsdPlan ssd_plan(const S6SsdProblem& p) {
   s.off_hs = off; off += align256(pn * (size_t)esize(p.io_dtype));
   s.off_cb = off; off += align256((size_t)(p.batch * s.K * p.ngroups) * p.chunk_size * p.chunk_size * 4);
   s.total = off;
+  const int64_t qt = p.chunk_size / 64;
+  s.nE = p.headdim * p.dstate / 1024;
+  s.off_dyw = off; off += p.has_z ? align256((size_t)(p.batch * p.seqlen * p.nheads * p.headdim) * esize(p.io_dtype)) : 0;
+  s.off_dst = off; off += align256(pn * (size_t)esize(p.io_dtype));
+  s.off_ddal = off; off += align256((size_t)(p.batch * p.nheads * s.K * s.nE) * 4);
+  s.off_ddtd = off; off += align256(bhkq);
+  s.off_dDp = off; off += align256((size_t)(p.batch * s.K * qt * p.nheads * p.headdim) * 4);
+  s.off_qv = off; off += align256(bhkq);
+  s.off_uv = off; off += align256(bhkq);
+  s.off_rs = off; off += align256(bhkq);
+  s.off_csp = off; off += align256(bhkq * (size_t)qt);
+  const size_t lgn = (size_t)(p.batch * p.seqlen * p.ngroups * p.dstate) * 4;
+  s.off_dBp = off; off += align256(lgn);
+  s.off_dCp = off; off += align256(lgn);
+  s.off_dcb = off; off += align256((size_t)(p.batch * s.K * p.ngroups) * p.chunk_size * p.chunk_size * 4);
+  s.off_dAp = off; off += align256((size_t)(p.batch * s.K * p.nheads) * 4);
+  s.off_dbp = off; off += align256((size_t)(p.batch * s.K * p.nheads) * 4);
+  s.total_bwd = off;
   return s;
 }
 
@@ -384,6 +406,36 @@ int ssd_check_rows(const void* ptr, const int64_t* s, int es, const char* name) 
   return S6_OK;
 }
 
+int ssd_check_inputs(const S6SsdProblem& p, const void* x, const int64_t* sx, const void* dt,
+                     const int64_t* sdt, const float* A, int64_t sA, const void* B,
+                     const int64_t* sB, const void* C, const int64_t* sC, const float* D,
+                     const int64_t* sD, const void* z, const int64_t* sz, const float* bias,
+                     const float* init, const int64_t* sinit, const int32_t* seq,
+                     const int64_t* sseq) {
+  int r;
+  if ((r = ssd_check_problem(p))) return r;
+  const int es = esize(p.io_dtype);
+  if ((r = check_ptr(x, "x")) || (r = check_strides(sx, 4, "x")) ||
+      (r = ssd_check_rows(x, sx, es, "x")) || (r = check_ptr(dt, "dt")) ||
+      (r = check_strides(sdt, 3, "dt")) || (r = check_ptr(A, "A")) || (r = check_ptr(B, "B")) ||
+      (r = check_strides(sB, 4, "B")) || (r = ssd_check_rows(B, sB, es, "B")) ||
+      (r = check_ptr(C, "C")) || (r = check_strides(sC, 4, "C")) ||
+      (r = ssd_check_rows(C, sC, es, "C")))
+    return r;
+  if (sA < 0) return fail(S6_E_INVALID, "A has a negative stride");
+  if (p.has_D && ((r = check_ptr(D, "D")) || (r = check_strides(sD, 2, "D")))) return r;
+  if (p.has_z && ((r = check_ptr(z, "z")) || (r = check_strides(sz, 4, "z")))) return r;
+  if (p.has_dt_bias && (r = check_ptr(bias, "dt_bias"))) return r;
+  if (p.has_initial_states &&
+      ((r = check_ptr(init, "initial_states")) || (r = check_strides(sinit, 4, "initial_states"))))
+    return r;
+  if (p.has_seq_idx && ((r = check_ptr(seq, "seq_idx")) || (r = check_strides(sseq, 2, "seq_idx"))))
+    return r;
+  return S6_OK;
+}
+
+s6::SsdK ssd_fill(const S6SsdFwdArgs& a, const SsdPlan& pl);
+
 }  // namespace
 
 extern "C" {
@@ -391,29 +443,13 @@ extern "C" {
 int s6_ssd_validate_fwd(const S6SsdFwdArgs* a) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
   const S6SsdProblem& p = a->p;
-  int r;
-  if ((r = ssd_check_problem(p))) return r;
-  const int es = esize(p.io_dtype);
-  if ((r = check_ptr(a->x, "x")) || (r = check_strides(a->x_stride, 4, "x")) ||
-      (r = ssd_check_rows(a->x, a->x_stride, es, "x")) ||
-      (r = check_ptr(a->dt, "dt")) || (r = check_strides(a->dt_stride, 3, "dt")) ||
-      (r = check_ptr(a->A, "A")) || (r = check_ptr(a->B, "B")) ||
-      (r = check_strides(a->B_stride, 4, "B")) || (r = ssd_check_rows(a->B, a->B_stride, es, "B")) ||
-      (r = check_ptr(a->C, "C")) || (r = check_strides(a->C_stride, 4, "C")) ||
-      (r = ssd_check_rows(a->C, a->C_stride, es, "C")) ||
-      (r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out")))
-    return r;
-  if (a->A_stride < 0) return fail(S6_E_INVALID, "A has a negative stride");
-  if (p.has_D && ((r = check_ptr(a->D, "D")) || (r = check_strides(a->D_stride, 2, "D")))) return r;
-  if (p.has_z && ((r = check_ptr(a->z, "z")) || (r = check_strides(a->z_stride, 4, "z")))) return r;
+  int r = ssd_check_inputs(p, a->x, a->x_stride, a->dt, a->dt_stride, a->A, a->A_stride, a->B,
+                           a->B_stride, a->C, a->C_stride, a->D, a->D_stride, a->z, a->z_stride,
+                           a->dt_bias, a->initial_states, a->initial_states_stride, a->seq_idx,
+                           a->seq_idx_stride);
+  if (r) return r;
+  if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out"))) return r;
   if (p.has_z && a->out_x && (r = check_strides(a->out_x_stride, 4, "out_x"))) return r;
-  if (p.has_dt_bias && (r = check_ptr(a->dt_bias, "dt_bias"))) return r;
-  if (p.has_initial_states && ((r = check_ptr(a->initial_states, "initial_states")) ||
-                               (r = check_strides(a->initial_states_stride, 4, "initial_states"))))
-    return r;
-  if (p.has_seq_idx && ((r = check_ptr(a->seq_idx, "seq_idx")) ||
-                        (r = check_strides(a->seq_idx_stride, 2, "seq_idx"))))
-    return r;
   const SsdPlan pl = ssd_plan(p);
   if (a->workspace == nullptr || a->workspace_bytes < pl.total)
     return fail(S6_E_WORKSPACE, "ssd forward workspace needs %zu bytes, got %zu", pl.total,
@@ -431,6 +467,107 @@ int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream) {
   if (r != S6_OK) return r;
   const S6SsdProblem& p = a->p;
   const SsdPlan pl = ssd_plan(p);
+  s6::SsdK k = ssd_fill(*a, pl);
+  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_fwd: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int s6_ssd_validate_bwd(const S6SsdBwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  const S6SsdProblem& p = a->p;
+  int r = ssd_check_inputs(p, a->x, a->x_stride, a->dt, a->dt_stride, a->A, a->A_stride, a->B,
+                           a->B_stride, a->C, a->C_stride, a->D, a->D_stride, a->z, a->z_stride,
+                           a->dt_bias, a->initial_states, a->initial_states_stride, a->seq_idx,
+                           a->seq_idx_stride);
+  if (r) return r;
+  const int es = esize(p.io_dtype);
+  if ((r = check_ptr(a->dout, "dout")) || (r = check_strides(a->dout_stride, 4, "dout")) ||
+      (r = ssd_check_rows(a->dout, a->dout_stride, es, "dout")) ||
+      (r = check_ptr(a->dx, "dx")) || (r = check_strides(a->dx_stride, 4, "dx")) ||
+      (r = check_ptr(a->ddt, "ddt")) || (r = check_strides(a->ddt_stride, 3, "ddt")) ||
+      (r = check_ptr(a->dA, "dA")) || (r = check_ptr(a->dB, "dB")) ||
+      (r = check_strides(a->dB_stride, 4, "dB")) || (r = check_ptr(a->dC, "dC")) ||
+      (r = check_strides(a->dC_stride, 4, "dC")))
+    return r;
+  if (p.has_D && (r = check_ptr(a->dD, "dD"))) return r;
+  if (p.has_z && ((r = check_ptr(a->out_x, "out_x")) || (r = check_strides(a->out_x_stride, 4, "out_x")) ||
+                  (r = check_ptr(a->dz, "dz")) || (r = check_strides(a->dz_stride, 4, "dz"))))
+    return r;
+  if (p.has_dt_bias && (r = check_ptr(a->ddt_bias, "ddt_bias"))) return r;
+  if (a->dfinal_states && (r = check_strides(a->dfinal_states_stride, 4, "dfinal_states"))) return r;
+  const SsdPlan pl = ssd_plan(p);
+  if (a->workspace == nullptr || a->workspace_bytes < pl.total_bwd)
+    return fail(S6_E_WORKSPACE, "ssd backward workspace needs %zu bytes, got %zu", pl.total_bwd,
+                a->workspace ? a->workspace_bytes : (size_t)0);
+  return ok();
+}
+
+size_t s6_ssd_bwd_workspace_bytes(const S6SsdProblem* p) {
+  if (p == nullptr || ssd_check_problem(*p) != S6_OK) return 0;
+  return ssd_plan(*p).total_bwd;
+}
+
+int s6_ssd_bwd(const S6SsdBwdArgs* a, void* stream) {
+  int r = s6_ssd_validate_bwd(a);
+  if (r != S6_OK) return r;
+  const S6SsdProblem& p = a->p;
+  const SsdPlan pl = ssd_plan(p);
+  S6SsdFwdArgs f{};
+  f.p = p;
+  f.x = a->x; f.dt = a->dt; f.A = a->A; f.A_stride = a->A_stride; f.B = a->B; f.C = a->C;
+  f.D = a->D; f.z = a->z; f.dt_bias = a->dt_bias; f.dt_bias_stride = a->dt_bias_stride;
+  f.initial_states = a->initial_states; f.seq_idx = a->seq_idx;
+  for (int i = 0; i < 4; ++i) {
+    f.x_stride[i] = a->x_stride[i]; f.B_stride[i] = a->B_stride[i]; f.C_stride[i] = a->C_stride[i];
+    f.z_stride[i] = a->z_stride[i]; f.initial_states_stride[i] = a->initial_states_stride[i];
+    f.out_x_stride[i] = a->out_x_stride[i];
+  }
+  for (int i = 0; i < 3; ++i) f.dt_stride[i] = a->dt_stride[i];
+  for (int i = 0; i < 2; ++i) { f.D_stride[i] = a->D_stride[i]; f.seq_idx_stride[i] = a->seq_idx_stride[i]; }
+  f.out_x = const_cast<void*>(a->out_x);
+  f.workspace = a->workspace; f.workspace_bytes = a->workspace_bytes;
+  s6::SsdK k = ssd_fill(f, pl);
+  char* ws = (char*)a->workspace;
+  k.final_states = nullptr;
+  k.dout = a->dout;
+  for (int i = 0; i < 4; ++i) {
+    k.sdout[i] = a->dout_stride[i]; k.sdx[i] = a->dx_stride[i];
+    k.sdBo[i] = a->dB_stride[i]; k.sdCo[i] = a->dC_stride[i];
+    k.sdz[i] = p.has_z ? a->dz_stride[i] : 0;
+    k.sdfinal[i] = a->dfinal_states ? a->dfinal_states_stride[i] : 0;
+  }
+  for (int i = 0; i < 3; ++i) k.sddt[i] = a->ddt_stride[i];
+  if (p.has_z) {
+    k.dyw = ws + pl.off_dyw;
+    k.dy = k.dyw;
+    const int64_t P = p.headdim, H = p.nheads, L = p.seqlen;
+    k.sdy[0] = L * H * P; k.sdy[1] = H * P; k.sdy[2] = P; k.sdy[3] = 1;
+  } else {
+    k.dy = a->dout;
+    for (int i = 0; i < 4; ++i) k.sdy[i] = a->dout_stride[i];
+  }
+  k.dz = p.has_z ? a->dz : nullptr; k.dx = a->dx; k.ddt = a->ddt; k.dBo = a->dB; k.dCo = a->dC;
+  k.dA = a->dA; k.dD = p.has_D ? a->dD : nullptr; k.ddt_bias = p.has_dt_bias ? a->ddt_bias : nullptr;
+  k.dinit = a->dinitial_states; k.dfinal = a->dfinal_states;
+  k.dhl = k.st;  // the chunk states are consumed by the recomputed state passing first
+  k.dst = ws + pl.off_dst; k.ddal = (float*)(ws + pl.off_ddal); k.nE = pl.nE;
+  k.ddtd = (float*)(ws + pl.off_ddtd); k.dDp = (float*)(ws + pl.off_dDp);
+  k.qv = (float*)(ws + pl.off_qv); k.uv = (float*)(ws + pl.off_uv); k.rs = (float*)(ws + pl.off_rs);
+  k.csp = (float*)(ws + pl.off_csp); k.dBp = (float*)(ws + pl.off_dBp); k.dCp = (float*)(ws + pl.off_dCp);
+  k.dcb = (float*)(ws + pl.off_dcb); k.dAp = (float*)(ws + pl.off_dAp); k.dbp = (float*)(ws + pl.off_dbp);
+  hipError_t e = s6::launch_ssd_bwd(k, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_bwd: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"
+
+namespace {
+
+s6::SsdK ssd_fill(const S6SsdFwdArgs& a0, const SsdPlan& pl) {
+  const S6SsdFwdArgs* a = &a0;
+  const S6SsdProblem& p = a->p;
   s6::SsdK k{};
   k.Bsz = p.batch; k.L = p.seqlen; k.H = p.nheads; k.P = p.headdim; k.G = p.ngroups;
   k.N = p.dstate; k.Q = p.chunk_size; k.K = pl.K; k.hpg = p.nheads / p.ngroups;
@@ -458,10 +595,12 @@ int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream) {
   char* ws = (char*)a->workspace;
   k.dtq = (float*)(ws + pl.off_dtq); k.dacs = (float*)(ws + pl.off_dacs);
   k.st = (float*)(ws + pl.off_st); k.hs = ws + pl.off_hs; k.cb = (float*)(ws + pl.off_cb);
-  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_fwd: %s", hipGetErrorString(e));
-  return ok();
+  return k;
 }
+
+}  // namespace
+
+extern "C" {
 
 int s6_validate_state_update(const S6StateUpdateArgs* a) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");

@@ -151,6 +151,32 @@ struct SsdK {
   float* st;    // [Bsz, K, H, P, N] chunk states
   void* hs;     // [Bsz, K, H, P, N] state entering each chunk (io dtype)
   float* cb;    // [Bsz, K, G, Q, Q] C B^T within each chunk (lower-triangle tiles written)
+  // ---- backward only ----
+  const void* dout; int64_t sdout[4];
+  const void* dy; int64_t sdy[4];     // dout * silu(z) (workspace) or dout itself
+  void* dyw;                          // [Bsz, L, H, P] io workspace for dy when z is given
+  void* dz; int64_t sdz[4];
+  void* dx; int64_t sdx[4];
+  void* ddt; int64_t sddt[3];
+  void* dBo; int64_t sdBo[4];
+  void* dCo; int64_t sdCo[4];
+  float* dA; float* dD; float* ddt_bias; float* dinit;   // dinit: [Bsz, H, P, N] contiguous
+  const float* dfinal; int64_t sdfinal[4];
+  float* dhl;     // [Bsz, K, H, P, N] gradient of each chunk's entering state from its outputs
+  void* dst;      // [Bsz, K, H, P, N] io: gradient of each chunk state
+  float* ddal;    // [Bsz, H, K, nE] partial gradients of S_last through the state passing
+  int64_t nE;     // element blocks of the state passing backward
+  float* ddtd;    // [Bsz, H, K, Q] direct dt gradient (x . (T1 + T2))
+  float* dDp;     // [Bsz * K * Q/64, H(, P)] partial dD
+  float* qv;      // [Bsz, H, K, Q] chunk-state decay terms
+  float* uv;      // [Bsz, H, K, Q] inter-chunk decay terms
+  float* dBp;     // [Bsz, L, G, N] fp32 dB from the chunk states
+  float* dCp;     // [Bsz, L, G, N] fp32 dC from the entering states
+  float* dcb;     // [Bsz, K, G, Q, Q] gradient of C B^T (lower-triangle tiles)
+  float* rs;      // [Bsz, H, K, Q] row sums of the intra-chunk decay terms
+  float* csp;     // [Bsz, H, K, Q/64, Q] column-sum partials per row tile
+  float* dAp;     // [Bsz * K, H] partial dA
+  float* dbp;     // [Bsz * K, H] partial ddt_bias
 };
 
 // Parameter block of the selective_state_update kernel (strides in elements).
@@ -194,8 +220,14 @@ hipError_t launch_conv_fwd(const ConvK& k, int io_dtype, int width, int vec, boo
                            hipStream_t st);
 hipError_t launch_conv_bwd(const ConvK& k, int io_dtype, int width, int vec, bool silu,
                            hipStream_t st);
-// s6_ssd.hip: the Mamba-2 SSD forward.
+// s6_ssd.hip: the Mamba-2 SSD forward; prep = dt processing, chunk states, state passing
+// and C B^T (shared with the backward, which recomputes them); dstates = the chunk-state
+// kernel in its backward mode (gradient of each chunk's entering state).
 hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st);
+hipError_t launch_ssd_prep(const SsdK& k, hipStream_t st);
+hipError_t launch_ssd_dstates(const SsdK& k, hipStream_t st);
+// s6_ssd_bwd.hip: the Mamba-2 SSD backward.
+hipError_t launch_ssd_bwd(const SsdK& k, hipStream_t st);
 // s6_ssu.hip: one decode step of the state.
 // rows: the state and A rows are contiguous and 16-byte aligned (vectorised row mapping).
 hipError_t launch_state_update(const SsuK& k, int state_dtype, bool softplus, bool rows,

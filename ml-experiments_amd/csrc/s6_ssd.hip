@@ -14,11 +14,7 @@
 //                     + D x_l, then * silu(z)                                       MFMA
 //                     (ssd_chunk_scan.py:43-185)
 //
-// MFMA use.  Every contraction runs on 16x16 output tiles with K = 32 per step: one
-// v_mfma_f32_16x16x32_bf16 for bf16 operands, eight v_mfma_f32_16x16x4_f32 for fp32.
-// Lane i of a wave holds A[i % 16][k(i, j)] and B[k(i, j)][i % 16] for items j < 8, with
-// k(i, j) = 8 (i / 16) + j (bf16) or i / 16 + 4 j (fp32), and D[4 (i / 16) + j][i % 16]
-// for j < 4.  Operands whose K axis is the sequence (x and B in the chunk state, x in the
+// MFMA operands (layout in s6_ssd_common.h): operands whose K axis is the sequence (x and B in the chunk state, x in the
 // chunk scan) are staged through LDS transposed, so each lane's 8 K-items are one 16-byte
 // LDS read; operands whose K axis is dstate (C, B in CB; C and the passed states in the
 // scan) are read straight from global memory, 16 bytes per lane.
@@ -27,87 +23,12 @@
 // the decayed CB of the chunk scan are rounded to the input type before the MFMA, the
 // passed states are stored in the input type, chunk states, CB and all accumulation are
 // fp32.
-#include "s6_internal.h"
-#include "ssd.h"
+#include "s6_ssd_common.h"
 
 namespace s6 {
 namespace {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
-constexpr int kKs = 32;            // sequence steps per MFMA K step (and per LDS slice)
-constexpr int kLp = kKs + 8;       // LDS row pitch in elements: 16-byte aligned rows
-constexpr int kThreads = 256;
-
-template <typename T> struct Mma;
-template <> struct Mma<bf16> {
-  typedef __bf16 Frag __attribute__((ext_vector_type(8)));
-  typedef uint16_t Raw;
-  static constexpr int kVe = 8;  // elements per 16-byte load
-  __device__ static inline int kidx(int lane, int j) { return 8 * (lane >> 4) + j; }
-  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
-    return *reinterpret_cast<const Frag*>(row_k0 + 8 * (lane >> 4));
-  }
-  __device__ static inline Frag from_float(const float (&v)[8]) {
-    Frag f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);
-    return f;
-  }
-  __device__ static inline Frag zero() {
-    Frag f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(0.f);
-    return f;
-  }
-  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-  }
-  __device__ static inline Raw to_raw(float v) {
-    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
-  }
-  __device__ static inline float from_raw(Raw r) { return __uint_as_float((uint32_t)r << 16); }
-};
-template <> struct Mma<float> {
-  struct Frag { float v[8]; };
-  typedef float Raw;
-  static constexpr int kVe = 4;
-  __device__ static inline int kidx(int lane, int j) { return (lane >> 4) + 4 * j; }
-  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
-    Frag f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f.v[j] = row_k0[(lane >> 4) + 4 * j];
-    return f;
-  }
-  __device__ static inline Frag from_float(const float (&v)[8]) {
-    Frag f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f.v[j] = v[j];
-    return f;
-  }
-  __device__ static inline Frag zero() {
-    Frag f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f.v[j] = 0.f;
-    return f;
-  }
-  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
-  }
-  __device__ static inline Raw to_raw(float v) { return v; }
-  __device__ static inline float from_raw(Raw r) { return r; }
-};
-
-// 16 bytes of a row, as kVe raw elements.
-template <typename T>
-__device__ inline void load16(const void* p, typename Mma<T>::Raw (&r)[Mma<T>::kVe]) {
-  const uint4 v = *reinterpret_cast<const uint4*>(p);
-  *reinterpret_cast<uint4*>(r) = v;
-}
-
-__device__ inline int32_t seq_at(const SsdK& k, int64_t b, int64_t t) {
-  return k.seq[b * k.sseq[0] + t * k.sseq[1]];
-}
+using namespace ssd;
 
 // ---- 1. dt processing and per-chunk cumulative decay ---------------------------------
 
@@ -136,7 +57,10 @@ __global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
 
 // ---- 2. chunk states -----------------------------------------------------------------
 
-template <typename T, int P, int N>
+// MODE 0 (forward): st_c = sum_l x_l (dt'_l e^{S_last - S_l} [seq_l == seq_last]) B_l^T.
+// MODE 1 (backward): dhl_c = sum_l dy_l (e^{S_l} [seq_l == seq before the chunk]) C_l^T,
+// the gradient of the state entering chunk c from the chunk's own outputs.
+template <typename T, int P, int N, int MODE>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   typedef Mma<T> M;
   typedef typename M::Raw Raw;
@@ -154,10 +78,14 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   const float* sq = k.dacs + ((b * k.H + hh) * k.K + c) * k.Q;
   const float* dq = k.dtq + ((b * k.H + hh) * k.K + c) * k.Q;
   const float s_last = sq[k.Q - 1];
-  const int32_t seq_last = k.has_seq ? seq_at(k, b, t0 + lim - 1) : 0;
+  const int32_t seq_ref = !k.has_seq ? 0
+                          : MODE == 0 ? seq_at(k, b, t0 + lim - 1)
+                                      : (c > 0 ? seq_at(k, b, t0 - 1) : 0);
   constexpr int ES = sizeof(Raw);
-  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
-  const char* bbase = (const char*)k.Bm + (b * k.sB[0] + t0 * k.sB[1] + g * k.sB[2]) * ES;
+  const int64_t* sxr = MODE == 0 ? k.sx : k.sdy;
+  const int64_t* sbr = MODE == 0 ? k.sB : k.sC;
+  const char* xbase = (const char*)(MODE == 0 ? k.x : k.dy) + (b * sxr[0] + t0 * sxr[1] + hh * sxr[2]) * ES;
+  const char* bbase = (const char*)(MODE == 0 ? k.Bm : k.Cm) + (b * sbr[0] + t0 * sbr[1] + g * sbr[2]) * ES;
 
   f4 acc[TPW];
 #pragma unroll
@@ -168,7 +96,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
     for (int e = tid; e < kKs * (P / VE); e += kThreads) {
       const int r = e / (P / VE), col = (e % (P / VE)) * VE;
       Raw v[VE];
-      if (l0 + r < lim) load16<T>(xbase + ((l0 + r) * k.sx[1] + col) * ES, v);
+      if (l0 + r < lim) load16<T>(xbase + ((l0 + r) * sxr[1] + col) * ES, v);
       else
 #pragma unroll
         for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
@@ -182,9 +110,9 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       float wl = 0.f;
       Raw v[VE];
       if (l < lim) {
-        load16<T>(bbase + (l * k.sB[1] + col) * ES, v);
-        wl = dq[l] * exp_split(s_last - sq[l]);
-        if (k.has_seq && seq_at(k, b, t0 + l) != seq_last) wl = 0.f;
+        load16<T>(bbase + (l * sbr[1] + col) * ES, v);
+        wl = MODE == 0 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
+        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) wl = 0.f;
       } else {
 #pragma unroll
         for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
@@ -205,7 +133,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
     }
     __syncthreads();
   }
-  float* out = k.st + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+  float* out = (MODE == 0 ? k.st : k.dhl) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int ti = w + 4 * i;
@@ -406,12 +334,12 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
 // ---- dispatch ------------------------------------------------------------------------
 
 template <typename T, int P, int N>
-hipError_t ssd_fwd_pn(const SsdK& k, hipStream_t st) {
+hipError_t ssd_prep_pn(const SsdK& k, hipStream_t st) {
   hipError_t e;
   hipLaunchKernelGGL((ssd_cumsum), dim3((unsigned)((k.H + kWave - 1) / kWave), (unsigned)k.K,
                      (unsigned)k.Bsz), dim3(kWave), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_chunk_state<T, P, N>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 0>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
                      dim3(kThreads), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_state_pass<T>), dim3((unsigned)((P * N + kThreads - 1) / kThreads),
@@ -420,39 +348,64 @@ hipError_t ssd_fwd_pn(const SsdK& k, hipStream_t st) {
   const int qt = (int)(k.Q / 64);
   hipLaunchKernelGGL((ssd_bmm<T, N>), dim3((unsigned)(qt * (qt + 1) / 2), (unsigned)k.K,
                      (unsigned)(k.Bsz * k.G)), dim3(kThreads), 0, st, k);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+template <typename T, int P, int N>
+hipError_t ssd_scan_pn(const SsdK& k, hipStream_t st) {
+  const int qt = (int)(k.Q / 64);
   hipLaunchKernelGGL((ssd_chunk_scan<T, P, N>), dim3((unsigned)qt, (unsigned)k.K,
                      (unsigned)(k.Bsz * k.H)), dim3(kThreads), 0, st, k);
   return hipGetLastError();
 }
 
-template <typename T, int P>
-hipError_t ssd_fwd_p(const SsdK& k, hipStream_t st) {
-  switch (k.N) {
-    case 32: return ssd_fwd_pn<T, P, 32>(k, st);
-    case 64: return ssd_fwd_pn<T, P, 64>(k, st);
-    case 128: return ssd_fwd_pn<T, P, 128>(k, st);
-    case 256: return ssd_fwd_pn<T, P, 256>(k, st);
-    default: return hipErrorInvalidValue;
-  }
+template <typename T, int P, int N>
+hipError_t ssd_dstates_pn(const SsdK& k, hipStream_t st) {
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 1>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
+                     dim3(kThreads), 0, st, k);
+  return hipGetLastError();
 }
 
-template <typename T>
-hipError_t ssd_fwd_t(const SsdK& k, hipStream_t st) {
-  switch (k.P) {
-    case 32: return ssd_fwd_p<T, 32>(k, st);
-    case 64: return ssd_fwd_p<T, 64>(k, st);
-    case 128: return ssd_fwd_p<T, 128>(k, st);
-    default: return hipErrorInvalidValue;
+// Calls F<T, P, N>::run(k, st) for the problem's dtype, headdim and dstate.
+#define S6_SSD_DISPATCH(FN)                                                               \
+  template <typename T, int P>                                                            \
+  hipError_t FN##_p(const SsdK& k, hipStream_t st) {                                      \
+    switch (k.N) {                                                                        \
+      case 32: return FN##_pn<T, P, 32>(k, st);                                           \
+      case 64: return FN##_pn<T, P, 64>(k, st);                                           \
+      case 128: return FN##_pn<T, P, 128>(k, st);                                         \
+      case 256: return FN##_pn<T, P, 256>(k, st);                                         \
+      default: return hipErrorInvalidValue;                                               \
+    }                                                                                     \
+  }                                                                                       \
+  template <typename T>                                                                   \
+  hipError_t FN##_t(const SsdK& k, hipStream_t st) {                                      \
+    switch (k.P) {                                                                        \
+      case 32: return FN##_p<T, 32>(k, st);                                               \
+      case 64: return FN##_p<T, 64>(k, st);                                               \
+      case 128: return FN##_p<T, 128>(k, st);                                             \
+      default: return hipErrorInvalidValue;                                               \
+    }                                                                                     \
+  }                                                                                       \
+  hipError_t FN(const SsdK& k, hipStream_t st) {                                          \
+    if (k.io == S6_BF16) return FN##_t<bf16>(k, st);                                      \
+    if (k.io == S6_F32) return FN##_t<float>(k, st);                                      \
+    return hipErrorInvalidValue;                                                          \
   }
-}
+
+S6_SSD_DISPATCH(ssd_prep)
+S6_SSD_DISPATCH(ssd_scan)
+S6_SSD_DISPATCH(ssd_dstates)
 
 }  // namespace
 
+hipError_t launch_ssd_prep(const SsdK& k, hipStream_t st) { return ssd_prep(k, st); }
+
+hipError_t launch_ssd_dstates(const SsdK& k, hipStream_t st) { return ssd_dstates(k, st); }
+
 hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st) {
-  if (k.io == S6_BF16) return ssd_fwd_t<bf16>(k, st);
-  if (k.io == S6_F32) return ssd_fwd_t<float>(k, st);
-  return hipErrorInvalidValue;
+  hipError_t e = ssd_prep(k, st);
+  return e != hipSuccess ? e : ssd_scan(k, st);
 }
 
 }  // namespace s6

@@ -1,0 +1,656 @@
+// Mamba-2 SSD backward, the computation of _mamba_chunk_scan_combined_bwd
+// (/root/reference/zoology/zoology/mixers/mamba_ssm/ops/triton/ssd_combined.py:335-452).
+// The forward quantities (dt', S, chunk states, entering states H, C B^T) are recomputed by
+// the forward's prep kernels.  With G = dy (dout * silu(z) when z is given), per batch b,
+// head h and chunk c, and the masks of the forward (mlast: same seq_idx as the chunk's last
+// step; mprev: same seq_idx as the step before the chunk; CB carries the pairwise mask):
+//
+//   ssd_bwd_gate       dy = dout silu(z), dz = dout y silu'(z)            (elementwise)
+//   (dstates)          dHl_c = sum_l mprev e^{S_l} G_l C_l^T                  MFMA
+//   ssd_state_pass_bwd dst_c = dH_{c+1}; dH_c = scale_c dH_{c+1} + dHl_c; dinit = dH_0;
+//                      the S_last gradient sum(dH_{c+1} scale_c H_c)
+//   ssd_bwd_dx         T2 = mlast e^{S_last - S_s} B_s dst^T, T1 = sum_{l>=s} CB e^{S_l-S_s} G_l
+//                      dx = dt'_s (T1 + T2) + D G_s; ddt'_s = x_s . (T1 + T2); dD parts  MFMA
+//   ssd_bwd_rows<4>    dB_s += sum_h mlast dt'_s e^{S_last-S_s} x_s^h dst^h; q_s per head MFMA
+//   ssd_bwd_rows<5>    dC_l += sum_h mprev e^{S_l} G_l^h H^h;             u_l per head  MFMA
+//   ssd_bwd_dcb        dM = G x^T per head; dCB = sum_h dM e^{S_l-S_s} dt'_s; row / column
+//                      sums of W = dM CB e^{S_l-S_s} dt'_s                             MFMA
+//   ssd_bwd_bmm<C|B>   dC += dCB B, dB += dCB^T C                                     MFMA
+//   ssd_bwd_dt         dS = u + rowsum(W) - colsum(W) - q (+ the S_last terms at the chunk
+//                      end); da = reverse cumsum of dS; ddt = A da + ddt'; through clamp,
+//                      softplus and bias; dA, ddt_bias parts
+//   ssd_bwd_reduce     dA, ddt_bias, dD in fixed order
+//
+// Every cross-block sum goes through a partial buffer reduced in fixed order: the backward
+// is deterministic (no atomics).
+#include "s6_ssd_common.h"
+
+namespace s6 {
+namespace {
+
+using namespace ssd;
+
+__device__ inline float wave_sum16(float v) {  // sum over the 16 lanes sharing lane / 16
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+__device__ inline int32_t seq_last_of(const SsdK& k, int64_t b, int64_t c) {
+  return seq_at(k, b, min((c + 1) * k.Q, k.L) - 1);
+}
+
+// ---- gate ----------------------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) ssd_bwd_gate(SsdK k) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= k.Bsz * k.L * k.H * k.P) return;
+  const int64_t p = i % k.P;
+  int64_t r = i / k.P;
+  const int64_t hh = r % k.H;
+  r /= k.H;
+  const int64_t t = r % k.L, b = r / k.L;
+  const float go = Elem<T>::load(k.dout, b * k.sdout[0] + t * k.sdout[1] + hh * k.sdout[2] + p);
+  const float zz = Elem<T>::load(k.z, b * k.sz[0] + t * k.sz[1] + hh * k.sz[2] + p);
+  const float y = Elem<T>::load(k.out_x, b * k.soutx[0] + t * k.soutx[1] + hh * k.soutx[2] + p);
+  const float sg = sigmoidf_(zz);
+  Elem<T>::store(k.dyw, i, go * zz * sg);
+  Elem<T>::store(k.dz, b * k.sdz[0] + t * k.sdz[1] + hh * k.sdz[2] + p,
+                 go * y * sg * fmaf(zz, 1.f - sg, 1.f));
+}
+
+// ---- state passing backward ----------------------------------------------------------
+
+constexpr int kSpbPer = 4;  // elements per thread
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) ssd_state_pass_bwd(SsdK k) {
+  typedef typename Mma<T>::Raw Raw;
+  __shared__ float red[kThreads / kWave];
+  const int64_t PN = k.P * k.N;
+  const int64_t eb = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  int64_t e[kSpbPer];
+  float dH[kSpbPer];
+#pragma unroll
+  for (int i = 0; i < kSpbPer; ++i) {
+    e[i] = eb * (kThreads * kSpbPer) + tid + i * kThreads;  // PN is a multiple of 1024
+    const int64_t p = e[i] / k.N, n = e[i] % k.N;
+    dH[i] = k.dfinal ? k.dfinal[b * k.sdfinal[0] + hh * k.sdfinal[1] + p * k.sdfinal[2] + n * k.sdfinal[3]] : 0.f;
+  }
+  const Raw* hs = (const Raw*)k.hs;
+  Raw* dst = (Raw*)k.dst;
+  for (int64_t c = k.K - 1; c >= 0; --c) {
+    float scale = exp_split(k.dacs[((b * k.H + hh) * k.K + c) * k.Q + k.Q - 1]);
+    if (k.has_seq) {
+      const int32_t prev = c > 0 ? seq_last_of(k, b, c - 1) : 0;
+      if (seq_last_of(k, b, c) != prev) scale = 0.f;
+    }
+    const int64_t o = ((b * k.K + c) * k.H + hh) * PN;
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSpbPer; ++i) {
+      dst[o + e[i]] = Mma<T>::to_raw(dH[i]);
+      part = fmaf(dH[i], Mma<T>::from_raw(hs[o + e[i]]), part);
+      dH[i] = fmaf(scale, dH[i], k.dhl[o + e[i]]);
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) part += __shfl_xor(part, m);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = part;
+    __syncthreads();
+    if (tid == 0) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < kThreads / kWave; ++w) s += red[w];
+      k.ddal[((b * k.H + hh) * k.K + c) * k.nE + eb] = s * scale;
+    }
+    __syncthreads();
+  }
+  if (k.dinit) {
+#pragma unroll
+    for (int i = 0; i < kSpbPer; ++i) k.dinit[(b * k.H + hh) * PN + e[i]] = dH[i];
+  }
+}
+
+// ---- dx, direct dt gradient, dD parts ------------------------------------------------
+
+template <typename T, int P, int N>
+__global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  constexpr int VE = M::kVe;
+  constexpr int PT = P / 16;
+  constexpr int ES = sizeof(Raw);
+  __shared__ __attribute__((aligned(16))) Raw gs[P][kLp];
+  __shared__ float sls[kKs];
+  __shared__ float dred[kThreads / kWave][P];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lt = blockIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.H, hh = blockIdx.z % k.H;
+  const int64_t g = hh / k.hpg;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  if (lt * 64 >= lim) return;  // whole block
+  const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
+  const float* sq = k.dacs + hrow;
+  const float* dq = k.dtq + hrow;
+  const int rowbase = lt * 64 + 16 * w;
+  const int row = rowbase + (lane & 15);
+  f4 acc[PT];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // T2: B_s dst^T, rows scaled by mlast e^{S_last - S_s}
+  {
+    const Raw* Brow = (const Raw*)k.Bm + b * k.sB[0] + (t0 + row) * k.sB[1] + g * k.sB[2];
+    const Raw* D2 = (const Raw*)k.dst + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+#pragma unroll
+    for (int n0 = 0; n0 < N; n0 += kKs) {
+      const typename M::Frag a = row < lim ? M::load_row(Brow + n0, lane) : M::zero();
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt)
+        M::mma(acc[pt], a, M::load_row(D2 + (pt * 16 + (lane & 15)) * N + n0, lane));
+    }
+    const float s_last = sq[k.Q - 1];
+    const int32_t seq_last = k.has_seq ? seq_last_of(k, b, c) : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = rowbase + 4 * (lane >> 4) + j;
+      float f = 0.f;
+      if (s < lim) {
+        f = exp_split(s_last - sq[s]);
+        if (k.has_seq && seq_at(k, b, t0 + s) != seq_last) f = 0.f;
+      }
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt) acc[pt][j] *= f;
+    }
+  }
+
+  // T1: sum_{l >= s} CB[l, s] e^{S_l - S_s} G_l
+  const float s_row = row < lim ? sq[row] : 0.f;
+  const float* cbcol = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + row;
+  const char* gbase = (const char*)k.dy + (b * k.sdy[0] + t0 * k.sdy[1] + hh * k.sdy[2]) * ES;
+  for (int l0 = lt * 64; l0 < lim; l0 += kKs) {
+    __syncthreads();
+    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      Raw v[VE];
+      if (l0 + r < lim) load16<T>(gbase + ((l0 + r) * k.sdy[1] + col) * ES, v);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) gs[col + q][r] = v[q];
+    }
+    if (tid < kKs) sls[tid] = sq[l0 + tid];
+    __syncthreads();
+    if (l0 + kKs - 1 >= rowbase) {  // wave-uniform
+      float m[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int li = M::kidx(lane, j);
+        const int l = l0 + li;
+        const bool on = l >= row && l < lim && row < lim;
+        const float v = cbcol[(int64_t)l * k.Q] * exp_split(sls[li] - s_row);
+        m[j] = on ? v : 0.f;
+      }
+      const typename M::Frag a = M::from_float(m);
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt)
+        M::mma(acc[pt], a, M::load_row(&gs[pt * 16 + (lane & 15)][0], lane));
+    }
+  }
+
+  // epilogue: dx, direct dt gradient, dD partial
+  float dd[PT];
+#pragma unroll
+  for (int pt = 0; pt < PT; ++pt) dd[pt] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s = rowbase + 4 * (lane >> 4) + j;
+    const bool valid = s < lim;
+    const int64_t t = t0 + (valid ? s : 0);
+    const float dts = valid ? dq[s] : 0.f;
+    float xsum = 0.f;
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      const int p = pt * 16 + (lane & 15);
+      const float xv = valid ? Elem<T>::load(k.x, b * k.sx[0] + t * k.sx[1] + hh * k.sx[2] + p) : 0.f;
+      const float gv = valid ? Elem<T>::load(k.dy, b * k.sdy[0] + t * k.sdy[1] + hh * k.sdy[2] + p) : 0.f;
+      const float a = acc[pt][j];
+      xsum = fmaf(xv, a, xsum);
+      dd[pt] = fmaf(gv, xv, dd[pt]);
+      if (valid) {
+        float dxv = dts * a;
+        if (k.has_D) {
+          const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + p * k.sD[1]] : k.Dp[hh * k.sD[0]];
+          dxv = fmaf(Dv, gv, dxv);
+        }
+        Elem<T>::store(k.dx, b * k.sdx[0] + t * k.sdx[1] + hh * k.sdx[2] + p, dxv);
+      }
+    }
+    xsum = wave_sum16(xsum);
+    if ((lane & 15) == 0 && valid) k.ddtd[hrow + s] = xsum;
+  }
+  if (k.has_D) {
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      float v = dd[pt];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (lane < 16) dred[w][pt * 16 + lane] = v;
+    }
+    __syncthreads();
+    const int64_t brow = (b * k.K + c) * (k.Q / 64) + lt;
+    if (k.D_hdim) {
+      for (int p = tid; p < P; p += kThreads)
+        k.dDp[(brow * k.H + hh) * P + p] = dred[0][p] + dred[1][p] + dred[2][p] + dred[3][p];
+    } else if (tid < kWave) {
+      float v = 0.f;
+      for (int p = tid; p < P; p += kWave) v += dred[0][p] + dred[1][p] + dred[2][p] + dred[3][p];
+#pragma unroll
+      for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+      if (tid == 0) k.dDp[brow * k.H + hh] = v;
+    }
+  }
+}
+
+// ---- per-group row products: dB from the chunk states (MODE 4), dC from the entering
+// states (MODE 5) ------------------------------------------------------------------------
+
+template <typename T, int P, int N, int MODE>
+__global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  constexpr int VE = M::kVe;
+  constexpr int NT = N / 16;
+  constexpr int ES = sizeof(Raw);
+  __shared__ __attribute__((aligned(16))) Raw ms[N][kLp];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lt = blockIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  if (lt * 64 >= lim) return;
+  const int rowbase = lt * 64 + 16 * w;
+  const int row = rowbase + (lane & 15);
+  const int64_t* sa = MODE == 4 ? k.sx : k.sdy;
+  const Raw* abase = (const Raw*)(MODE == 4 ? k.x : k.dy) + b * sa[0] + (t0 + row) * sa[1];
+  const Raw* side = (const Raw*)(MODE == 4 ? k.Bm : k.Cm);
+  const int64_t* ss = MODE == 4 ? k.sB : k.sC;
+  const int32_t seq_ref = !k.has_seq ? 0
+                          : MODE == 4 ? seq_last_of(k, b, c) : (c > 0 ? seq_at(k, b, t0 - 1) : 0);
+  f4 tot[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) tot[i] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t hh = g * k.hpg; hh < (g + 1) * k.hpg; ++hh) {
+    const Raw* mat = (const Raw*)(MODE == 4 ? k.dst : k.hs) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+    f4 acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < P; p0 += kKs) {
+      __syncthreads();
+      for (int e = tid; e < kKs * (N / VE); e += kThreads) {  // mat rows p0..p0+31 -> ms[n][p]
+        const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+        Raw v[VE];
+        load16<T>(mat + (p0 + r) * N + col, v);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) ms[col + q][r] = v[q];
+      }
+      __syncthreads();
+      const typename M::Frag a = row < lim ? M::load_row(abase + hh * sa[2] + p0, lane) : M::zero();
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) M::mma(acc[nt], a, M::load_row(&ms[nt * 16 + (lane & 15)][0], lane));
+    }
+    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
+    const float* sq = k.dacs + hrow;
+    const float* dq = k.dtq + hrow;
+    const float s_last = sq[k.Q - 1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      float f = 0.f;
+      if (l < lim) {
+        f = MODE == 4 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
+        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) f = 0.f;
+      }
+      float sv = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        acc[nt][j] *= f;
+        const float sd = l < lim ? Elem<T>::load(side, b * ss[0] + (t0 + l) * ss[1] + g * ss[2] + nt * 16 + (lane & 15)) : 0.f;
+        sv = fmaf(sd, acc[nt][j], sv);
+        tot[nt][j] += acc[nt][j];
+      }
+      sv = wave_sum16(sv);
+      if ((lane & 15) == 0 && l < lim) (MODE == 4 ? k.qv : k.uv)[hrow + l] = sv;
+    }
+  }
+  float* outp = MODE == 4 ? k.dBp : k.dCp;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = rowbase + 4 * (lane >> 4) + j;
+    if (l >= lim) continue;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      outp[((b * k.L + t0 + l) * k.G + g) * N + nt * 16 + (lane & 15)] = tot[nt][j];
+  }
+}
+
+// ---- dCB and the intra-chunk decay terms ---------------------------------------------
+
+template <typename T, int P, int QT>
+__global__ void __launch_bounds__(kThreads) ssd_bwd_dcb(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  __shared__ float csred[kThreads / kWave][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int I = blockIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  if (I * 64 >= lim) return;
+  const int rowbase = I * 64 + 16 * w;
+  const int row = rowbase + (lane & 15);
+  const float* cbm = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
+  f4 dcb[QT][4];
+#pragma unroll
+  for (int J = 0; J < QT; ++J)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) dcb[J][ct] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t hh = g * k.hpg; hh < (g + 1) * k.hpg; ++hh) {
+    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
+    const float* sq = k.dacs + hrow;
+    const float* dq = k.dtq + hrow;
+    const Raw* grow = (const Raw*)k.dy + b * k.sdy[0] + (t0 + row) * k.sdy[1] + hh * k.sdy[2];
+    const Raw* xb = (const Raw*)k.x + b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2];
+    float sl[4], rsum[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      sl[j] = l < lim ? sq[l] : 0.f;
+      rsum[j] = 0.f;
+    }
+#pragma unroll
+    for (int J = 0; J < QT; ++J) {
+      if (J > I) break;  // block-uniform
+      f4 dM[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) dM[ct] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p0 = 0; p0 < P; p0 += kKs) {
+        const typename M::Frag a = row < lim ? M::load_row(grow + p0, lane) : M::zero();
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int s = J * 64 + ct * 16 + (lane & 15);
+          const typename M::Frag bf = s < lim ? M::load_row(xb + s * k.sx[1] + p0, lane) : M::zero();
+          M::mma(dM[ct], a, bf);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int s = J * 64 + ct * 16 + (lane & 15);
+        const float ssv = sq[s], dsv = dq[s];
+        float colsum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int l = rowbase + 4 * (lane >> 4) + j;
+          const bool on = s <= l && l < lim && s < lim;
+          const float ev = exp_split(sl[j] - ssv);
+          const float dme = on ? dM[ct][j] * ev * dsv : 0.f;
+          dcb[J][ct][j] += dme;
+          const float wv = dme * cbm[(int64_t)l * k.Q + s];
+          rsum[j] += wv;
+          colsum += wv;
+        }
+        colsum += __shfl_xor(colsum, 16);
+        colsum += __shfl_xor(colsum, 32);
+        if (lane < 16) csred[w][ct * 16 + lane] = colsum;
+      }
+      __syncthreads();
+      if (tid < 64)
+        k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + J * 64 + tid] =
+            csred[0][tid] + csred[1][tid] + csred[2][tid] + csred[3][tid];
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      const float v = wave_sum16(rsum[j]);
+      if ((lane & 15) == 0 && l < lim) k.rs[hrow + l] = v;
+    }
+  }
+  float* out = k.dcb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
+#pragma unroll
+  for (int J = 0; J < QT; ++J) {
+    if (J > I) break;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int l = rowbase + 4 * (lane >> 4) + j;
+        const int s = J * 64 + ct * 16 + (lane & 15);
+        float v = dcb[J][ct][j];
+        if (!(l < lim && s < lim)) v = 0.f;
+        else if (k.has_seq && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
+        out[(int64_t)l * k.Q + s] = v;
+      }
+    }
+  }
+}
+
+// ---- dC += dCB B (MODE 0), dB += dCB^T C (MODE 1) -------------------------------------
+
+template <typename T, int N, int MODE>
+__global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
+  typedef Mma<T> M;
+  typedef typename M::Raw Raw;
+  constexpr int VE = M::kVe;
+  constexpr int NT = N / 16;
+  constexpr int ES = sizeof(Raw);
+  __shared__ __attribute__((aligned(16))) Raw os[N][kLp];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lt = blockIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  if (lt * 64 >= lim) return;
+  const int rowbase = lt * 64 + 16 * w;
+  const int row = rowbase + (lane & 15);
+  const float* dcbm = k.dcb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
+  const int64_t* so = MODE == 0 ? k.sB : k.sC;  // the staged operand: B for dC, C for dB
+  const char* obase = (const char*)(MODE == 0 ? k.Bm : k.Cm) + (b * so[0] + t0 * so[1] + g * so[2]) * ES;
+  f4 acc[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+  const int k0 = MODE == 0 ? 0 : lt * 64;
+  const int k1 = MODE == 0 ? min(lt * 64 + 64, lim) : lim;
+  for (int s0 = k0; s0 < k1; s0 += kKs) {
+    __syncthreads();
+    for (int e = tid; e < kKs * (N / VE); e += kThreads) {
+      const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+      Raw v[VE];
+      if (s0 + r < lim) load16<T>(obase + ((s0 + r) * so[1] + col) * ES, v);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) os[col + q][r] = v[q];
+    }
+    __syncthreads();
+    const bool reach = MODE == 0 ? s0 <= rowbase + 15 : s0 + kKs - 1 >= rowbase;  // wave-uniform
+    if (reach) {
+      float m[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int kk = s0 + M::kidx(lane, j);
+        const bool on = row < lim && kk < lim && (MODE == 0 ? kk <= row : kk >= row);
+        const float v = MODE == 0 ? dcbm[(int64_t)row * k.Q + kk] : dcbm[(int64_t)kk * k.Q + row];
+        m[j] = on ? v : 0.f;
+      }
+      const typename M::Frag a = M::from_float(m);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) M::mma(acc[nt], a, M::load_row(&os[nt * 16 + (lane & 15)][0], lane));
+    }
+  }
+  const float* part = MODE == 0 ? k.dCp : k.dBp;
+  void* outp = MODE == 0 ? k.dCo : k.dBo;
+  const int64_t* sop = MODE == 0 ? k.sdCo : k.sdBo;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = rowbase + 4 * (lane >> 4) + j;
+    if (l >= lim) continue;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = nt * 16 + (lane & 15);
+      const float v = acc[nt][j] + part[((b * k.L + t0 + l) * k.G + g) * N + n];
+      Elem<T>::store(outp, b * sop[0] + (t0 + l) * sop[1] + g * sop[2] + n, v);
+    }
+  }
+}
+
+// ---- dt, dA, ddt_bias ----------------------------------------------------------------
+
+__global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
+  const int64_t idx = (int64_t)blockIdx.x * kWave + threadIdx.x;
+  if (idx >= k.Bsz * k.H * k.K) return;
+  const int64_t c = idx % k.K;
+  const int64_t hh = (idx / k.K) % k.H;
+  const int64_t b = idx / (k.K * k.H);
+  const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
+  const int64_t t0 = c * k.Q;
+  const int lim = (int)min(k.Q, k.L - t0);
+  const int QT = (int)(k.Q / 64);
+  float ddal = 0.f;
+  for (int64_t e = 0; e < k.nE; ++e) ddal += k.ddal[((b * k.H + hh) * k.K + c) * k.nE + e];
+  float qsum = 0.f;
+  for (int l = 0; l < lim; ++l) qsum += k.qv[hrow + l];
+  const float A = k.A[hh * k.sA];
+  const float bias = k.has_bias ? k.bias[hh * k.sbias] : 0.f;
+  float da = 0.f, dAacc = 0.f, dbacc = 0.f;
+  for (int j = (int)k.Q - 1; j >= 0; --j) {
+    float dS = j == k.Q - 1 ? ddal + qsum : 0.f;
+    if (j < lim) {
+      float cs = 0.f;
+      // row tiles I >= tile(j) that hold steps of this chunk (later tiles never ran)
+      for (int I = j / 64; I < (lim + 63) / 64; ++I)
+        cs += k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + j];
+      dS += k.uv[hrow + j] + k.rs[hrow + j] - cs - k.qv[hrow + j];
+    }
+    da += dS;
+    if (j < lim) {
+      const float dtp = k.dtq[hrow + j];
+      float g = fmaf(A, da, k.ddtd[hrow + j]);
+      dAacc = fmaf(dtp, da, dAacc);
+      const float v = load_any(k.dt, b * k.sdt[0] + (t0 + j) * k.sdt[1] + hh * k.sdt[2], k.io) + bias;
+      const float sp = k.softplus ? softplus20(v) : v;
+      if (sp < k.dt_min || sp > k.dt_max) g = 0.f;
+      if (k.softplus && v <= 20.f) g *= sigmoidf_(v);
+      store_any(k.ddt, b * k.sddt[0] + (t0 + j) * k.sddt[1] + hh * k.sddt[2], g, k.io);
+      dbacc += g;
+    }
+  }
+  k.dAp[(b * k.K + c) * k.H + hh] = dAacc;
+  k.dbp[(b * k.K + c) * k.H + hh] = dbacc;
+}
+
+__global__ void __launch_bounds__(kThreads) ssd_bwd_reduce(SsdK k) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t rows = k.Bsz * k.K;
+  if (i < k.H) {
+    float a = 0.f, db = 0.f;
+    for (int64_t r = 0; r < rows; ++r) {
+      a += k.dAp[r * k.H + i];
+      db += k.dbp[r * k.H + i];
+    }
+    k.dA[i] = a;
+    if (k.ddt_bias) k.ddt_bias[i] = db;
+  }
+  if (k.has_D) {
+    const int64_t nd = k.D_hdim ? k.H * k.P : k.H;
+    if (i < nd) {
+      const int64_t qt = k.Q / 64;
+      float s = 0.f;
+      for (int64_t r = 0; r < rows * qt; ++r) {
+        const int64_t lt = r % qt, c = (r / qt) % k.K;
+        if (lt * 64 >= min(k.Q, k.L - c * k.Q)) continue;  // tile past the sequence end: no partial
+        s += k.dDp[r * nd + i];
+      }
+      k.dD[i] = s;
+    }
+  }
+}
+
+// ---- dispatch ------------------------------------------------------------------------
+
+template <typename T, int P, int N>
+hipError_t ssd_bwd_pn(const SsdK& k, hipStream_t st) {
+  hipError_t e;
+  const unsigned qt = (unsigned)(k.Q / 64);
+  const dim3 blk(kThreads);
+  if (k.has_z) {
+    const int64_t n = k.Bsz * k.L * k.H * k.P;
+    hipLaunchKernelGGL((ssd_bwd_gate<T>), dim3((unsigned)((n + kThreads - 1) / kThreads)), blk, 0, st, k);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if ((e = launch_ssd_dstates(k, st)) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_state_pass_bwd<T>), dim3((unsigned)k.nE, (unsigned)k.H, (unsigned)k.Bsz), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_dx<T, P, N>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.H)), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 4>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  switch (qt) {
+    case 1: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 1>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
+    case 2: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 2>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
+    case 4: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 4>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
+    default: return hipErrorInvalidValue;
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 0>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 1>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int64_t nt = k.Bsz * k.H * k.K;
+  hipLaunchKernelGGL((ssd_bwd_dt), dim3((unsigned)((nt + kWave - 1) / kWave)), dim3(kWave), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int64_t nr = k.H * k.P;
+  hipLaunchKernelGGL((ssd_bwd_reduce), dim3((unsigned)((nr + kThreads - 1) / kThreads)), blk, 0, st, k);
+  return hipGetLastError();
+}
+
+template <typename T, int P>
+hipError_t ssd_bwd_p(const SsdK& k, hipStream_t st) {
+  switch (k.N) {
+    case 32: return ssd_bwd_pn<T, P, 32>(k, st);
+    case 64: return ssd_bwd_pn<T, P, 64>(k, st);
+    case 128: return ssd_bwd_pn<T, P, 128>(k, st);
+    case 256: return ssd_bwd_pn<T, P, 256>(k, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T>
+hipError_t ssd_bwd_t(const SsdK& k, hipStream_t st) {
+  switch (k.P) {
+    case 32: return ssd_bwd_p<T, 32>(k, st);
+    case 64: return ssd_bwd_p<T, 64>(k, st);
+    case 128: return ssd_bwd_p<T, 128>(k, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_ssd_bwd(const SsdK& k, hipStream_t st) {
+  hipError_t e = launch_ssd_prep(k, st);
+  if (e != hipSuccess) return e;
+  if (k.io == S6_BF16) return ssd_bwd_t<bf16>(k, st);
+  if (k.io == S6_F32) return ssd_bwd_t<float>(k, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace s6

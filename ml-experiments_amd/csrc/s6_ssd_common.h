@@ -1,0 +1,93 @@
+// Shared device code of the Mamba-2 SSD kernels (s6_ssd.hip forward, s6_ssd_bwd.hip
+// backward): the MFMA operand abstraction and small helpers.
+//
+// MFMA use.  Every contraction runs on 16x16 output tiles with K = 32 per step: one
+// v_mfma_f32_16x16x32_bf16 for bf16 operands, eight v_mfma_f32_16x16x4_f32 for fp32.
+// Lane i of a wave holds A[i % 16][k(i, j)] and B[k(i, j)][i % 16] for items j < 8, with
+// k(i, j) = 8 (i / 16) + j (bf16) or i / 16 + 4 j (fp32), and D[4 (i / 16) + j][i % 16]
+// for j < 4.
+#pragma once
+#include "s6_internal.h"
+#include "ssd.h"
+
+namespace s6 {
+namespace ssd {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr int kKs = 32;            // sequence steps per MFMA K step (and per LDS slice)
+constexpr int kLp = kKs + 8;       // LDS row pitch in elements: 16-byte aligned rows
+constexpr int kThreads = 256;
+
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+  typedef __bf16 Frag __attribute__((ext_vector_type(8)));
+  typedef uint16_t Raw;
+  static constexpr int kVe = 8;  // elements per 16-byte load
+  __device__ static inline int kidx(int lane, int j) { return 8 * (lane >> 4) + j; }
+  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
+    return *reinterpret_cast<const Frag*>(row_k0 + 8 * (lane >> 4));
+  }
+  __device__ static inline Frag from_float(const float (&v)[8]) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);
+    return f;
+  }
+  __device__ static inline Frag zero() {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(0.f);
+    return f;
+  }
+  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  __device__ static inline Raw to_raw(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  }
+  __device__ static inline float from_raw(Raw r) { return __uint_as_float((uint32_t)r << 16); }
+};
+template <> struct Mma<float> {
+  struct Frag { float v[8]; };
+  typedef float Raw;
+  static constexpr int kVe = 4;
+  __device__ static inline int kidx(int lane, int j) { return (lane >> 4) + 4 * j; }
+  __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = row_k0[(lane >> 4) + 4 * j];
+    return f;
+  }
+  __device__ static inline Frag from_float(const float (&v)[8]) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = v[j];
+    return f;
+  }
+  __device__ static inline Frag zero() {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = 0.f;
+    return f;
+  }
+  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
+  }
+  __device__ static inline Raw to_raw(float v) { return v; }
+  __device__ static inline float from_raw(Raw r) { return r; }
+};
+
+// 16 bytes of a row, as kVe raw elements.
+template <typename T>
+__device__ inline void load16(const void* p, typename Mma<T>::Raw (&r)[Mma<T>::kVe]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  *reinterpret_cast<uint4*>(r) = v;
+}
+
+__device__ inline int32_t seq_at(const SsdK& k, int64_t b, int64_t t) {
+  return k.seq[b * k.sseq[0] + t * k.sseq[1]];
+}
+
+}  // namespace ssd
+}  // namespace s6

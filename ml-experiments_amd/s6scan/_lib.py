@@ -168,6 +168,35 @@ class S6SsdFwdArgs(ctypes.Structure):
     ]
 
 
+class S6SsdBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("p", S6SsdProblem),
+        ("x", _vp), ("x_stride", _a(4)),
+        ("dt", _vp), ("dt_stride", _a(3)),
+        ("A", _vp), ("A_stride", _i64),
+        ("B", _vp), ("B_stride", _a(4)),
+        ("C", _vp), ("C_stride", _a(4)),
+        ("D", _vp), ("D_stride", _a(2)),
+        ("z", _vp), ("z_stride", _a(4)),
+        ("dt_bias", _vp), ("dt_bias_stride", _i64),
+        ("initial_states", _vp), ("initial_states_stride", _a(4)),
+        ("seq_idx", _vp), ("seq_idx_stride", _a(2)),
+        ("dout", _vp), ("dout_stride", _a(4)),
+        ("out_x", _vp), ("out_x_stride", _a(4)),
+        ("dfinal_states", _vp), ("dfinal_states_stride", _a(4)),
+        ("dx", _vp), ("dx_stride", _a(4)),
+        ("ddt", _vp), ("ddt_stride", _a(3)),
+        ("dA", _vp),
+        ("dB", _vp), ("dB_stride", _a(4)),
+        ("dC", _vp), ("dC_stride", _a(4)),
+        ("dD", _vp),
+        ("dz", _vp), ("dz_stride", _a(4)),
+        ("ddt_bias", _vp),
+        ("dinitial_states", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 EXPORTS = {
     "s6_abi_version": (ctypes.c_int, []),
     "s6_last_error": (ctypes.c_char_p, []),
@@ -187,6 +216,9 @@ EXPORTS = {
     "s6_ssd_validate_fwd": (ctypes.c_int, [ctypes.POINTER(S6SsdFwdArgs)]),
     "s6_ssd_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6SsdProblem)]),
     "s6_ssd_fwd": (ctypes.c_int, [ctypes.POINTER(S6SsdFwdArgs), ctypes.c_void_p]),
+    "s6_ssd_validate_bwd": (ctypes.c_int, [ctypes.POINTER(S6SsdBwdArgs)]),
+    "s6_ssd_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6SsdProblem)]),
+    "s6_ssd_bwd": (ctypes.c_int, [ctypes.POINTER(S6SsdBwdArgs), ctypes.c_void_p]),
     "s6_validate_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs)]),
     "s6_selective_state_update": (ctypes.c_int, [ctypes.POINTER(S6StateUpdateArgs), ctypes.c_void_p]),
 }

@@ -106,3 +106,59 @@ def test_ssd_rejects_unsupported_shapes():
     t, kw = make(1, 64, 1, 48, 1, 32, torch.float32, seed=1)
     with pytest.raises(RuntimeError, match="headdim"):
         ssd_forward(**{k: v.to(DEV) for k, v in t.items()}, chunk_size=64, **kw)
+
+
+GRAD_CASES = [  # batch, L, H, P, G, N, chunk, opts
+    (2, 300, 4, 64, 2, 64, 64, ("D", "z", "bias")),
+    (1, 512, 2, 32, 1, 128, 128, ("init", "seq", "D_hdim", "final")),
+    (2, 256, 3, 128, 3, 32, 256, ("limit", "bias")),
+    (1, 200, 2, 64, 1, 256, 64, ("z", "init", "bias", "final")),
+    (2, 130, 4, 32, 2, 32, 64, ("seq", "z", "D")),
+]
+
+
+def check_grad(a, b, dtype, what):
+    if dtype == torch.float32:
+        assert_close(a, b, 1e-4, 1e-4 * rms(b), what)
+    else:
+        d = a.detach().float().cpu() - b.detach().float()
+        rel = (d.norm() / b.detach().float().norm()).item()
+        assert rel < 3e-2, f"{what}: norm-wise relative error {rel:.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", GRAD_CASES)
+def test_ssd_backward_matches_autograd(case, dtype):
+    batch, L, H, P, G, N, Q, opts = case
+    t, kw = make(batch, L, H, P, G, N, dtype, seed=L + 3 * N, opts=opts)
+    final = "final" in opts
+    g = torch.Generator().manual_seed(L)
+    dy = torch.randn(batch, L, H, P, generator=g)
+    dfin = torch.randn(batch, H, P, N, generator=g)
+    names = [k for k, v in t.items() if v.is_floating_point()]
+    gpu = {k: (v.to(DEV).requires_grad_(True) if k in names else v.to(DEV)) for k, v in t.items()}
+    res = mamba_chunk_scan_combined(**gpu, chunk_size=Q, return_final_states=final, **kw)
+    out, fin = res if final else (res, None)
+    loss = (out.float() * dy.to(DEV)).sum() + ((fin * dfin.to(DEV)).sum() if final else 0.0)
+    loss.backward()
+    cpu = {k: (v.double().requires_grad_(True) if k in names else v) for k, v in t.items()}
+    ref, _, ref_fin = ssd_chunked_ref(**cpu, chunk_size=Q, compute_dtype=torch.float64, **kw)
+    rloss = (ref * dy.double()).sum() + ((ref_fin * dfin.double()).sum() if final else 0.0)
+    rloss.backward()
+    for k in names:
+        assert gpu[k].grad is not None, k
+        assert gpu[k].grad.shape == t[k].shape and gpu[k].grad.dtype == t[k].dtype, k
+        check_grad(gpu[k].grad, cpu[k].grad, dtype, "d" + k)
+
+
+def test_ssd_backward_is_deterministic():
+    t, kw = make(2, 300, 4, 64, 2, 64, torch.bfloat16, seed=5, opts=("D", "z", "bias", "init"))
+    dy = torch.randn(2, 300, 4, 64, generator=torch.Generator().manual_seed(6)).to(DEV)
+    grads = []
+    for _ in range(2):
+        gpu = {k: v.to(DEV).requires_grad_(True) for k, v in t.items()}
+        out = mamba_chunk_scan_combined(**gpu, chunk_size=64, **kw)
+        (out.float() * dy).sum().backward()
+        grads.append([gpu[k].grad.clone() for k in sorted(gpu)])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
