@@ -2,7 +2,7 @@
 """Benchmark of the MI355X S6 selective scan; prints ONE JSON line on stdout.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload fwd1|fwdbwd3|fwd2|fwdbwd4|mixer1|mamba3|decode|copyref]
+                    [--workload fwd1|fwdbwd3|fwd2|fwdbwd4|mixer1|mamba3|decode|ssd2|copyref]
 
 Default workload ``fwd1``: the forward scan at B=32, L=4096, D=256, N=16, bf16 I/O with
 fp32 state (the configuration the headline metric is quoted on), called like a [B, L, D]
@@ -11,7 +11,8 @@ return_last_state=True)``.  ``fwdbwd3`` times forward + backward at B=8, L=8192,
 N=16 bf16; ``fwd2`` the fp32 N=64 long-sequence forward; ``fwdbwd4`` the packed varlen
 forward + backward; ``mixer1`` the SSMMixer S6 core at the fwd1 shape; ``mamba3`` one
 training step of the fused Mamba block (MambaInnerFn) at the fwdbwd3 shape; ``decode`` the
-selective_state_update decode step (batch 64, d_inner 1536), graph-launched.
+selective_state_update decode step (batch 64, d_inner 1536), graph-launched; ``ssd2`` the
+Mamba-2 SSD (mamba_chunk_scan_combined) forward and forward + backward at Mamba-2 defaults.
 
 * value: algorithmic HBM bytes of one step (each tensor once) / wall time per step, with
   the inputs resident in HBM.  Three independent input sets rotate so the 256 MB
@@ -50,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="fwd1",
                     choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "mamba3",
-                             "decode", "copyref"])
+                             "decode", "ssd2", "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -346,6 +347,113 @@ def run_decode(torch, args):
     print(json.dumps(res), flush=True)
 
 
+SSD2 = dict(batch=8, seqlen=8192, nheads=24, headdim=64, ngroups=1, dstate=128, chunk=256)
+
+
+def ssd_bytes(c, backward):
+    """HBM bytes of the SSD path, each tensor once (bf16 activations): x, dt, B, C read and
+    out written; the backward also reads dout and writes dx, ddt, dB, dC."""
+    B, L, H, P, G, N = c["batch"], c["seqlen"], c["nheads"], c["headdim"], c["ngroups"], c["dstate"]
+    fwd = 2 * (2 * B * L * H * P + B * L * H + 2 * B * L * G * N)
+    if not backward:
+        return fwd
+    return fwd + 2 * (2 * B * L * H * P + B * L * H + 2 * B * L * G * N)
+
+
+def ssd_flops(c):
+    """Forward MFMA flops: chunk states and the entering-state term (2 B L H P N each), the
+    intra-chunk product (2 B L H P Q / 2 on average, causal) and C B^T (B L G Q N)."""
+    B, L, H, P, G, N, Q = (c["batch"], c["seqlen"], c["nheads"], c["headdim"], c["ngroups"],
+                           c["dstate"], c["chunk"])
+    return 4 * B * L * H * P * N + B * L * H * P * Q + B * L * G * Q * N
+
+
+def run_ssd(torch, args):
+    """Workload ssd2: Mamba-2's default SSD layer (headdim 64, dstate 128, chunk 256, one
+    group, D per head, dt bias + softplus, no z: the RMSNorm variant, mamba2.py:30-56,
+    209-225) at 24 heads (d_model 768), batch 8, seqlen 8192, bf16: one forward and one
+    forward + backward of mamba_chunk_scan_combined."""
+    from s6scan.ssd_combined import mamba_chunk_scan_combined
+    c = SSD2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, L, H, P, G, N, Q = (c["batch"], c["seqlen"], c["nheads"], c["headdim"], c["ngroups"],
+                           c["dstate"], c["chunk"])
+    g = torch.Generator("cpu").manual_seed(3)
+    bf = torch.bfloat16
+    r = lambda *s: torch.randn(*s, generator=g)
+    sets = []
+    for _ in range(2):
+        sets.append(dict(x=r(B, L, H, P).to(dev, bf), dt=(0.5 * r(B, L, H) - 2.0).to(dev, bf),
+                         B=r(B, L, G, N).to(dev, bf), C=r(B, L, G, N).to(dev, bf),
+                         dy=r(B, L, H, P).to(dev, bf)))
+    A = (-torch.exp(torch.rand(H, generator=g) * 2.77)).to(dev).requires_grad_(True)
+    D = torch.randn(H, generator=g).to(dev).requires_grad_(True)
+    bias = (0.3 * torch.randn(H, generator=g)).to(dev).requires_grad_(True)
+
+    def fwd(i):
+        s_ = sets[i % 2]
+        with torch.no_grad():
+            mamba_chunk_scan_combined(s_["x"], s_["dt"], A, s_["B"], s_["C"], Q, D=D,
+                                      dt_bias=bias, dt_softplus=True)
+
+    def fwdbwd(i):
+        s_ = sets[i % 2]
+        leaves = {k: s_[k].detach().requires_grad_(True) for k in ("x", "dt", "B", "C")}
+        out = mamba_chunk_scan_combined(leaves["x"], leaves["dt"], A, leaves["B"], leaves["C"], Q,
+                                        D=D, dt_bias=bias, dt_softplus=True)
+        out.backward(s_["dy"])
+
+    res_t = {}
+    for name, fn in (("fwd", fwd), ("fwdbwd", fwdbwd)):
+        for i in range(args.warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            fn(i)
+        torch.cuda.synchronize()
+        res_t[name] = (time.perf_counter() - t0) * 1e3 / args.steps
+    tokch = B * L * H * P
+    fl = ssd_flops(c)
+    res = {
+        "metric": "Mamba-2 SSD (mamba_chunk_scan_combined) fwd+bwd Mtok·ch/s at 1 GPU",
+        "value": round(tokch / (res_t["fwdbwd"] * 1e-3) / 1e6, 2), "unit": "Mtok·ch/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(res_t["fwdbwd"], 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal inputs, Mamba-2 A init range [-16, -1])",
+        "config": {"workload": (f"ssd2: batch {B}, seqlen {L}, nheads {H}, headdim {P}, ngroups "
+                                f"{G}, dstate {N}, chunk {Q}; D per head, dt bias + softplus, no z")},
+        "fwd_ms": round(res_t["fwd"], 5),
+        "fwd_mtok_ch_per_s": round(tokch / (res_t["fwd"] * 1e-3) / 1e6, 2),
+        "fwd_achieved": {"hbm_GBps_io_only": round(ssd_bytes(c, False) / (res_t["fwd"] * 1e-3) / 1e9, 2),
+                         "mfma_TFLOPs": round(fl / (res_t["fwd"] * 1e-3) / 1e12, 2)},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        from oracle.ssd_ref import ssd_chunked_ref
+        torch.set_num_threads(os.cpu_count() or 1)
+        Ls = 2048
+        s_ = sets[0]
+        cpu = {k: s_[k][:1, :Ls].float().cpu() for k in ("x", "dt", "B", "C")}
+        Ac, Dc, bc = A.detach().cpu(), D.detach().cpu(), bias.detach().cpu()
+        call = lambda n: ssd_chunked_ref(cpu["x"][:, :n], cpu["dt"][:, :n], Ac, cpu["B"][:, :n],
+                                         cpu["C"][:, :n], Q, D=Dc, dt_bias=bc, dt_softplus=True)
+        call(Q)  # untimed: first-call allocation and thread-pool start-up
+        reps, t = 0, time.perf_counter()
+        while reps < 200 and (reps == 0 or time.perf_counter() - t < 10.0):
+            call(Ls)
+            reps += 1
+        sec = time.perf_counter() - t
+        res["cpu_baseline"] = {"value": round(reps * Ls * H * P / sec / 1e6, 4), "unit": "Mtok·ch/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": (f"restated reference chunked forward (ssd_chunked_ref, "
+                                          f"fp32 torch ops), batch 1, seqlen {Ls}, {reps} calls: "
+                                          f"{sec:.2f} s")}
+    print(json.dumps(res), flush=True)
+
+
 def copy_reference(torch, steps):
     """Plain device-to-device copy of a known size (1 GiB read + 1 GiB written per launch).
     Profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between those
@@ -379,6 +487,9 @@ def main():
         return
     if args.workload == "decode":
         run_decode(torch, args)
+        return
+    if args.workload == "ssd2":
+        run_ssd(torch, args)
         return
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward

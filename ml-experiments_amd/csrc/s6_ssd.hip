@@ -3,6 +3,7 @@
 // triton/ssd_combined.py:281-332), in five kernels:
 //
 //   ssd_cumsum        dt -> dt' = clamp(softplus(dt + bias)), S = cumsum(dt' A) per chunk
+//                     (a wave scan per chunk and head)
 //                     (ssd_chunk_state.py:34-84 semantics)
 //   ssd_chunk_state   st_c[p, n] = sum_l x_l[p] (dt'_l e^{S_last - S_l}) B_l[n]     MFMA
 //                     (ssd_chunk_state.py:177-266)
@@ -32,26 +33,41 @@ using namespace ssd;
 
 // ---- 1. dt processing and per-chunk cumulative decay ---------------------------------
 
+// One wave per (batch, chunk, head): lane i holds steps 4i .. 4i+3 (chunk <= 256), sums
+// them, and an inclusive wave scan of the lane totals gives each lane its prefix.
 __global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
-  const int64_t hh = (int64_t)blockIdx.x * kWave + threadIdx.x;
-  if (hh >= k.H) return;
-  const int64_t c = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int64_t c = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const float A = k.A[hh * k.sA];
   const float bias = k.has_bias ? k.bias[hh * k.sbias] : 0.f;
   const int64_t row = ((b * k.H + hh) * k.K + c) * k.Q;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
-  float acc = 0.f;
-  for (int l = 0; l < (int)k.Q; ++l) {
-    float v = 0.f;
+  float v[4], a[4];
+  float tot = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int l = 4 * lane + q;
+    v[q] = 0.f;
     if (l < lim) {
-      v = load_any(k.dt, b * k.sdt[0] + (t0 + l) * k.sdt[1] + hh * k.sdt[2], k.io) + bias;
-      if (k.softplus) v = softplus20(v);
-      v = fminf(fmaxf(v, k.dt_min), k.dt_max);
+      v[q] = load_any(k.dt, b * k.sdt[0] + (t0 + l) * k.sdt[1] + hh * k.sdt[2], k.io) + bias;
+      if (k.softplus) v[q] = softplus20(v[q]);
+      v[q] = fminf(fmaxf(v[q], k.dt_min), k.dt_max);
     }
-    acc += v * A;
-    k.dtq[row + l] = v;
-    k.dacs[row + l] = acc;
+    tot += v[q] * A;
+    a[q] = tot;
+  }
+  float incl = tot;  // inclusive scan of the lane totals
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const float u = __shfl_up(incl, m);
+    if (lane >= m) incl += u;
+  }
+  const float pre = incl - tot;
+  if (4 * lane < k.Q) {
+    *reinterpret_cast<float4*>(k.dtq + row + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(k.dacs + row + 4 * lane) =
+        make_float4(pre + a[0], pre + a[1], pre + a[2], pre + a[3]);
   }
 }
 
@@ -336,8 +352,8 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
 template <typename T, int P, int N>
 hipError_t ssd_prep_pn(const SsdK& k, hipStream_t st) {
   hipError_t e;
-  hipLaunchKernelGGL((ssd_cumsum), dim3((unsigned)((k.H + kWave - 1) / kWave), (unsigned)k.K,
-                     (unsigned)k.Bsz), dim3(kWave), 0, st, k);
+  hipLaunchKernelGGL((ssd_cumsum), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz), dim3(kWave),
+                     0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 0>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
                      dim3(kThreads), 0, st, k);

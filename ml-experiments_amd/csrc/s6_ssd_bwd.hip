@@ -512,33 +512,58 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
 
 // ---- dt, dA, ddt_bias ----------------------------------------------------------------
 
+// One wave per (batch, head, chunk): lane i holds steps 4i .. 4i+3.  da_j = sum_{k >= j} dS_k
+// is a suffix scan: per-lane suffix sums plus a wave scan of the lane totals from the top.
 __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
-  const int64_t idx = (int64_t)blockIdx.x * kWave + threadIdx.x;
-  if (idx >= k.Bsz * k.H * k.K) return;
-  const int64_t c = idx % k.K;
-  const int64_t hh = (idx / k.K) % k.H;
-  const int64_t b = idx / (k.K * k.H);
+  const int lane = threadIdx.x;
+  const int64_t c = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
   const int QT = (int)(k.Q / 64);
+  const int nI = (lim + 63) / 64;  // row tiles that ran
   float ddal = 0.f;
-  for (int64_t e = 0; e < k.nE; ++e) ddal += k.ddal[((b * k.H + hh) * k.K + c) * k.nE + e];
+  for (int64_t e = lane; e < k.nE; e += kWave) ddal += k.ddal[((b * k.H + hh) * k.K + c) * k.nE + e];
+  float qv[4], dS[4];
   float qsum = 0.f;
-  for (int l = 0; l < lim; ++l) qsum += k.qv[hrow + l];
-  const float A = k.A[hh * k.sA];
-  const float bias = k.has_bias ? k.bias[hh * k.sbias] : 0.f;
-  float da = 0.f, dAacc = 0.f, dbacc = 0.f;
-  for (int j = (int)k.Q - 1; j >= 0; --j) {
-    float dS = j == k.Q - 1 ? ddal + qsum : 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * lane + q;
+    qv[q] = j < lim ? k.qv[hrow + j] : 0.f;
+    qsum += qv[q];
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    qsum += __shfl_xor(qsum, m);
+    ddal += __shfl_xor(ddal, m);
+  }
+  float tot = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * lane + q;
+    float d = j == k.Q - 1 ? ddal + qsum : 0.f;
     if (j < lim) {
       float cs = 0.f;
-      // row tiles I >= tile(j) that hold steps of this chunk (later tiles never ran)
-      for (int I = j / 64; I < (lim + 63) / 64; ++I)
-        cs += k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + j];
-      dS += k.uv[hrow + j] + k.rs[hrow + j] - cs - k.qv[hrow + j];
+      for (int I = j / 64; I < nI; ++I) cs += k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + j];
+      d += k.uv[hrow + j] + k.rs[hrow + j] - cs - qv[q];
     }
-    da += dS;
+    dS[q] = d;
+    tot += d;
+  }
+  float incl = tot;  // inclusive scan of lane totals from the last lane down
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const float u = __shfl_down(incl, m);
+    if (lane + m < kWave) incl += u;
+  }
+  float da = incl - tot;  // sum over the lanes above
+  const float A = k.A[hh * k.sA];
+  const float bias = k.has_bias ? k.bias[hh * k.sbias] : 0.f;
+  float dAacc = 0.f, dbacc = 0.f;
+#pragma unroll
+  for (int q = 3; q >= 0; --q) {
+    const int j = 4 * lane + q;
+    da += dS[q];
     if (j < lim) {
       const float dtp = k.dtq[hrow + j];
       float g = fmaf(A, da, k.ddtd[hrow + j]);
@@ -551,35 +576,44 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
       dbacc += g;
     }
   }
-  k.dAp[(b * k.K + c) * k.H + hh] = dAacc;
-  k.dbp[(b * k.K + c) * k.H + hh] = dbacc;
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    dAacc += __shfl_xor(dAacc, m);
+    dbacc += __shfl_xor(dbacc, m);
+  }
+  if (lane == 0) {
+    k.dAp[(b * k.K + c) * k.H + hh] = dAacc;
+    k.dbp[(b * k.K + c) * k.H + hh] = dbacc;
+  }
 }
 
-__global__ void __launch_bounds__(kThreads) ssd_bwd_reduce(SsdK k) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+// One wave per output (dA[h], ddt_bias[h], dD[h(, p)]): lanes take every 64th partial row,
+// then a fixed-order wave sum.
+__global__ void __launch_bounds__(kWave) ssd_bwd_reduce(SsdK k) {
+  const int lane = threadIdx.x;
+  const int64_t o = blockIdx.x;
   const int64_t rows = k.Bsz * k.K;
-  if (i < k.H) {
-    float a = 0.f, db = 0.f;
-    for (int64_t r = 0; r < rows; ++r) {
-      a += k.dAp[r * k.H + i];
-      db += k.dbp[r * k.H + i];
-    }
-    k.dA[i] = a;
-    if (k.ddt_bias) k.ddt_bias[i] = db;
-  }
-  if (k.has_D) {
+  float s = 0.f;
+  if (o < 2 * k.H) {
+    const float* src = o < k.H ? k.dAp : k.dbp;
+    const int64_t h = o % k.H;
+    for (int64_t r = lane; r < rows; r += kWave) s += src[r * k.H + h];
+  } else {
+    const int64_t i = o - 2 * k.H;
     const int64_t nd = k.D_hdim ? k.H * k.P : k.H;
-    if (i < nd) {
-      const int64_t qt = k.Q / 64;
-      float s = 0.f;
-      for (int64_t r = 0; r < rows * qt; ++r) {
-        const int64_t lt = r % qt, c = (r / qt) % k.K;
-        if (lt * 64 >= min(k.Q, k.L - c * k.Q)) continue;  // tile past the sequence end: no partial
-        s += k.dDp[r * nd + i];
-      }
-      k.dD[i] = s;
+    const int64_t qt = k.Q / 64;
+    for (int64_t r = lane; r < rows * qt; r += kWave) {
+      const int64_t lt = r % qt, c = (r / qt) % k.K;
+      if (lt * 64 >= min(k.Q, k.L - c * k.Q)) continue;  // tile past the sequence end: no partial
+      s += k.dDp[r * nd + i];
     }
   }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) s += __shfl_xor(s, m);
+  if (lane != 0) return;
+  if (o < k.H) k.dA[o] = s;
+  else if (o < 2 * k.H) { if (k.ddt_bias) k.ddt_bias[o - k.H] = s; }
+  else k.dD[o - 2 * k.H] = s;
 }
 
 // ---- dispatch ------------------------------------------------------------------------
@@ -614,11 +648,10 @@ hipError_t ssd_bwd_pn(const SsdK& k, hipStream_t st) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 1>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int64_t nt = k.Bsz * k.H * k.K;
-  hipLaunchKernelGGL((ssd_bwd_dt), dim3((unsigned)((nt + kWave - 1) / kWave)), dim3(kWave), 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_dt), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz), dim3(kWave), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int64_t nr = k.H * k.P;
-  hipLaunchKernelGGL((ssd_bwd_reduce), dim3((unsigned)((nr + kThreads - 1) / kThreads)), blk, 0, st, k);
+  const int64_t nout = 2 * k.H + (k.has_D ? (k.D_hdim ? k.H * k.P : k.H) : 0);
+  hipLaunchKernelGGL((ssd_bwd_reduce), dim3((unsigned)nout), dim3(kWave), 0, st, k);
   return hipGetLastError();
 }
 
