@@ -23,7 +23,8 @@
  *   initial_states       : [batch, nheads, headdim, dstate] fp32, any strides (optional)
  *   seq_idx              : [batch, seqlen] int32, any strides (optional)
  *   final_states         : [batch, nheads, headdim, dstate] fp32 contiguous (optional out)
- * Rows read with vector loads (x, z, B, C, out) must start on 16-byte boundaries.
+ * Rows accessed with 16-byte vector loads and stores (x, z, B, C, out, out_x, dout) need a
+ * unit last stride and must start on 16-byte boundaries.
  * Supported: headdim in {32, 64, 128}, dstate in {32, 64, 128, 256}, chunk_size in
  * {64, 128, 256}, io_dtype bf16 or fp32.  Errors and streams as in s6scan.h.
  */

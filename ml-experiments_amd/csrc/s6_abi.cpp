@@ -424,7 +424,9 @@ int ssd_check_inputs(const S6SsdProblem& p, const void* x, const int64_t* sx, co
     return r;
   if (sA < 0) return fail(S6_E_INVALID, "A has a negative stride");
   if (p.has_D && ((r = check_ptr(D, "D")) || (r = check_strides(sD, 2, "D")))) return r;
-  if (p.has_z && ((r = check_ptr(z, "z")) || (r = check_strides(sz, 4, "z")))) return r;
+  if (p.has_z && ((r = check_ptr(z, "z")) || (r = check_strides(sz, 4, "z")) ||
+                   (r = ssd_check_rows(z, sz, es, "z"))))
+    return r;
   if (p.has_dt_bias && (r = check_ptr(bias, "dt_bias"))) return r;
   if (p.has_initial_states &&
       ((r = check_ptr(init, "initial_states")) || (r = check_strides(sinit, 4, "initial_states"))))
@@ -448,8 +450,14 @@ int s6_ssd_validate_fwd(const S6SsdFwdArgs* a) {
                            a->dt_bias, a->initial_states, a->initial_states_stride, a->seq_idx,
                            a->seq_idx_stride);
   if (r) return r;
-  if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out"))) return r;
-  if (p.has_z && a->out_x && (r = check_strides(a->out_x_stride, 4, "out_x"))) return r;
+  const int es = esize(p.io_dtype);
+  if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out")) ||
+      (r = ssd_check_rows(a->out, a->out_stride, es, "out")))
+    return r;
+  if (p.has_z && a->out_x &&
+      ((r = check_strides(a->out_x_stride, 4, "out_x")) ||
+       (r = ssd_check_rows(a->out_x, a->out_x_stride, es, "out_x"))))
+    return r;
   const SsdPlan pl = ssd_plan(p);
   if (a->workspace == nullptr || a->workspace_bytes < pl.total)
     return fail(S6_E_WORKSPACE, "ssd forward workspace needs %zu bytes, got %zu", pl.total,

@@ -76,6 +76,11 @@ __global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
 // MODE 0 (forward): st_c = sum_l x_l (dt'_l e^{S_last - S_l} [seq_l == seq_last]) B_l^T.
 // MODE 1 (backward): dhl_c = sum_l dy_l (e^{S_l} [seq_l == seq before the chunk]) C_l^T,
 // the gradient of the state entering chunk c from the chunk's own outputs.
+//
+// Software pipeline over 32-step slices: the global loads of slice i + 1 (x rows, B rows and
+// their weights) go to registers while the MFMAs of slice i run; the registers are written,
+// transposed and weighted, to the other half of a double LDS buffer, one barrier per slice.
+// (With a single buffer, when two would not fit in 64 KB, a second barrier guards it.)
 template <typename T, int P, int N, int MODE>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   typedef Mma<T> M;
@@ -84,8 +89,12 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   constexpr int NTN = N / 16;
   constexpr int NT = (P / 16) * NTN;
   constexpr int TPW = (NT + 3) / 4;
-  __shared__ __attribute__((aligned(16))) Raw xs[P][kLp];
-  __shared__ __attribute__((aligned(16))) Raw bs[N][kLp];
+  constexpr int ES = sizeof(Raw);
+  constexpr int NB = 2 * (P + N) * kLp * ES <= 65536 ? 2 : 1;
+  constexpr int XC = kKs * (P / VE), BC = kKs * (N / VE);       // 16-byte chunks per slice
+  constexpr int XL = (XC + kThreads - 1) / kThreads, BL = (BC + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(16))) Raw xs[NB][P][kLp];
+  __shared__ __attribute__((aligned(16))) Raw bs[NB][N][kLp];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t c = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const int64_t g = hh / k.hpg;
@@ -97,57 +106,80 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   const int32_t seq_ref = !k.has_seq ? 0
                           : MODE == 0 ? seq_at(k, b, t0 + lim - 1)
                                       : (c > 0 ? seq_at(k, b, t0 - 1) : 0);
-  constexpr int ES = sizeof(Raw);
   const int64_t* sxr = MODE == 0 ? k.sx : k.sdy;
   const int64_t* sbr = MODE == 0 ? k.sB : k.sC;
   const char* xbase = (const char*)(MODE == 0 ? k.x : k.dy) + (b * sxr[0] + t0 * sxr[1] + hh * sxr[2]) * ES;
   const char* bbase = (const char*)(MODE == 0 ? k.Bm : k.Cm) + (b * sbr[0] + t0 * sbr[1] + g * sbr[2]) * ES;
 
+  Raw xv[XL][VE], bv[BL][VE];
+  float wv[BL];
+  // Loads of the slice starting at l0 into registers; rows past the sequence end read as 0.
+  auto fetch = [&](int l0) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      if (e < XC && l0 + r < lim) load16<T>(xbase + ((l0 + r) * sxr[1] + col) * ES, xv[i]);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) xv[i][q] = M::to_raw(0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int e = tid + i * kThreads;
+      const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+      const int l = l0 + r;
+      wv[i] = 0.f;
+      if (e < BC && l < lim) {
+        load16<T>(bbase + (l * sbr[1] + col) * ES, bv[i]);
+        wv[i] = MODE == 0 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
+        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) wv[i] = 0.f;
+      } else {
+#pragma unroll
+        for (int q = 0; q < VE; ++q) bv[i][q] = M::to_raw(0.f);
+      }
+    }
+  };
+
   f4 acc[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int l0 = 0; l0 < lim; l0 += kKs) {
-    // x rows l0..l0+31 -> xs[p][l]; zero past the sequence end
-    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
-      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
-      Raw v[VE];
-      if (l0 + r < lim) load16<T>(xbase + ((l0 + r) * sxr[1] + col) * ES, v);
-      else
+  const int nsl = (lim + kKs - 1) / kKs;
+  fetch(0);
+  for (int sl = 0; sl < nsl; ++sl) {
+    const int buf = NB == 2 ? (sl & 1) : 0;
+    if (NB == 1 && sl > 0) __syncthreads();  // the single buffer is consumed
 #pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < XC) {
+        const int r = e / (P / VE), col = (e % (P / VE)) * VE;
 #pragma unroll
-      for (int q = 0; q < VE; ++q) xs[col + q][r] = v[q];
-    }
-    // B rows scaled by dt'_l e^{S_last - S_l} (0 outside the last sequence) -> bs[n][l]
-    for (int e = tid; e < kKs * (N / VE); e += kThreads) {
-      const int r = e / (N / VE), col = (e % (N / VE)) * VE;
-      const int l = l0 + r;
-      float wl = 0.f;
-      Raw v[VE];
-      if (l < lim) {
-        load16<T>(bbase + (l * sbr[1] + col) * ES, v);
-        wl = MODE == 0 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
-        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) wl = 0.f;
-      } else {
-#pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+        for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
       }
+    }
 #pragma unroll
-      for (int q = 0; q < VE; ++q) bs[col + q][r] = M::to_raw(M::from_raw(v[q]) * wl);
+    for (int i = 0; i < BL; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < BC) {
+        const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+#pragma unroll
+        for (int q = 0; q < VE; ++q) bs[buf][col + q][r] = M::to_raw(M::from_raw(bv[i][q]) * wv[i]);
+      }
     }
     __syncthreads();
+    if (sl + 1 < nsl) fetch((sl + 1) * kKs);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int ti = w + 4 * i;
       if (ti < NT) {
         const int pt = ti / NTN, nt = ti % NTN;
-        const typename M::Frag a = M::load_row(&xs[pt * 16 + (lane & 15)][0], lane);
-        const typename M::Frag bf = M::load_row(&bs[nt * 16 + (lane & 15)][0], lane);
+        const typename M::Frag a = M::load_row(&xs[buf][pt * 16 + (lane & 15)][0], lane);
+        const typename M::Frag bf = M::load_row(&bs[buf][nt * 16 + (lane & 15)][0], lane);
         M::mma(acc[i], a, bf);
       }
     }
-    __syncthreads();
   }
   float* out = (MODE == 0 ? k.st : k.dhl) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
 #pragma unroll
@@ -234,6 +266,15 @@ __global__ void __launch_bounds__(kThreads) ssd_bmm(SsdK k) {
 
 // ---- 5. chunk scan -------------------------------------------------------------------
 
+// Block: 64 rows (steps) of one chunk and head, 4 waves of 16 rows, all of headdim.
+// The intra-chunk product runs as a software pipeline over stages of SUB MFMA K steps: the
+// x rows and the wave's CB values of stage i + 1 are loaded to registers while stage i's
+// MFMAs run, x goes transposed to the other half of a double LDS buffer, one barrier per
+// stage.  The decay e^{S_l - S_s} is exp2((S_l - S_s) log2 e), as the reference's tl.exp:
+// the difference is taken first, since the cumsums themselves can reach thousands and
+// scaling them before subtracting would add their rounding to the exponent.  y is staged
+// through LDS (reusing the x buffer) so that the D skip, the z gate and the stores run on
+// 16-byte rows.
 template <typename T, int P, int N>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   typedef Mma<T> M;
@@ -241,8 +282,18 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   constexpr int VE = M::kVe;
   constexpr int PT = P / 16;
   constexpr int ES = sizeof(Raw);
-  __shared__ __attribute__((aligned(16))) Raw xs[P][kLp];
-  __shared__ float sls[kKs], dls[kKs];
+  constexpr int SUB = (ES == 2 || P <= 64) ? 2 : 1;       // MFMA K steps per stage
+  constexpr int KST = SUB * kKs;                           // steps per stage
+  constexpr int LP = KST + 8;                              // LDS row pitch, 16-byte rows
+  constexpr int XC = KST * (P / VE);                       // 16-byte x chunks per stage
+  constexpr int XL = (XC + kThreads - 1) / kThreads;
+  constexpr int YP = P + 4;                                // y staging pitch (floats)
+  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4;
+  constexpr int SM_BYTES = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SM_BYTES];
+  __shared__ float sls[2][KST], dls[2][KST];
+  Raw (*xs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
+  float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lt = blockIdx.x;
   const int64_t c = blockIdx.y, b = blockIdx.z / k.H, hh = blockIdx.z % k.H;
@@ -254,6 +305,37 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   const float* dq = k.dtq + ((b * k.H + hh) * k.K + c) * k.Q;
   const int rowbase = lt * 64 + 16 * w;
   const int row = rowbase + (lane & 15);  // A-operand row of this lane
+  const float* cbrow = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + (int64_t)row * k.Q;
+  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
+  const int s_end = min(lt * 64 + 64, lim);
+  const int nst = (s_end + KST - 1) / KST;
+
+  Raw xv[XL][VE];
+  float cbv[SUB][8];
+  float sv = 0.f, dv = 0.f;
+  auto fetch = [&](int s0) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      if (e < XC && s0 + r < lim) load16<T>(xbase + ((s0 + r) * k.sx[1] + col) * ES, xv[i]);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) xv[i][q] = M::to_raw(0.f);
+    }
+    if (tid < KST) {  // rows of the chunk past lim hold S and dt' of 0 / the last step
+      sv = sq[s0 + tid];
+      dv = dq[s0 + tid];
+    }
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks) {
+      const bool reach = s0 + ks * kKs <= rowbase + 15;  // wave-uniform
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cbv[ks][j] = reach ? cbrow[s0 + ks * kKs + M::kidx(lane, j)] : 0.f;
+    }
+  };
+  fetch(0);
+
   f4 acc[PT];
 #pragma unroll
   for (int i = 0; i < PT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
@@ -285,65 +367,94 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
 
   // (b) within the chunk: sum_{s <= l} CB[l, s] e^{S_l - S_s} dt'_s x_s
   const float s_row = row < lim ? sq[row] : 0.f;
-  const float* cbrow = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + (int64_t)row * k.Q;
-  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
-  const int s_end = min(lt * 64 + 64, lim);
-  for (int s0 = 0; s0 < s_end; s0 += kKs) {
-    __syncthreads();  // the previous slice is consumed
-    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
-      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
-      Raw v[VE];
-      if (s0 + r < lim) load16<T>(xbase + ((s0 + r) * k.sx[1] + col) * ES, v);
-      else
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const int s0 = st * KST;
 #pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < XC) {
+        const int r = e / (P / VE), col = (e % (P / VE)) * VE;
 #pragma unroll
-      for (int q = 0; q < VE; ++q) xs[col + q][r] = v[q];
-    }
-    if (tid < kKs) {
-      sls[tid] = sq[s0 + tid];
-      dls[tid] = dq[s0 + tid];
-    }
-    __syncthreads();
-    if (s0 <= rowbase + 15) {  // wave-uniform: the slice reaches this wave's rows
-      float m[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int si = M::kidx(lane, j);
-        const int s = s0 + si;
-        const float cbv = cbrow[s];
-        const bool on = s <= row && row < lim && s < lim;
-        const float v = cbv * exp_split(s_row - sls[si]) * dls[si];
-        m[j] = on ? v : 0.f;
+        for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
       }
-      const typename M::Frag a = M::from_float(m);
+    }
+    if (tid < KST) {
+      sls[buf][tid] = sv;
+      dls[buf][tid] = dv;
+    }
+    float cbc[SUB][8];
 #pragma unroll
-      for (int pt = 0; pt < PT; ++pt)
-        M::mma(acc[pt], a, M::load_row(&xs[pt * 16 + (lane & 15)][0], lane));
+    for (int ks = 0; ks < SUB; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cbc[ks][j] = cbv[ks][j];
+    __syncthreads();
+    if (st + 1 < nst) fetch(s0 + KST);
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks) {
+      if (s0 + ks * kKs <= rowbase + 15) {  // wave-uniform: the slice reaches this wave's rows
+        float m[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int si = ks * kKs + M::kidx(lane, j);
+          const int s = s0 + si;
+          const bool on = s <= row && row < lim && s < lim;
+          const float v = cbc[ks][j] * fast_exp2((s_row - sls[buf][si]) * kLog2e) * dls[buf][si];
+          m[j] = on ? v : 0.f;
+        }
+        const typename M::Frag a = M::from_float(m);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+          M::mma(acc[pt], a, M::load_row(&xs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+      }
     }
   }
 
-  // (c) D skip, z gate, stores
+  // (c) y through LDS, then the D skip, z gate and 16-byte stores
+  __syncthreads();  // every wave is done reading x from the buffer ys reuses
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int l = rowbase + 4 * (lane >> 4) + j;
+  for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ys[16 * w + 4 * (lane >> 4) + j][pt * 16 + (lane & 15)] = acc[pt][j];
+  __syncthreads();
+  constexpr int YC = 64 * (P / VE);
+  for (int e = tid; e < YC; e += kThreads) {
+    const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+    const int l = lt * 64 + r;
     if (l >= lim) continue;
     const int64_t t = t0 + l;
+    float y[VE];
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) {
-      const int p = pt * 16 + (lane & 15);
-      float y = acc[pt][j];
-      if (k.has_D) {
-        const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + p * k.sD[1]] : k.Dp[hh * k.sD[0]];
-        y = fmaf(Dv, Elem<T>::load(k.x, b * k.sx[0] + t * k.sx[1] + hh * k.sx[2] + p), y);
+    for (int q = 0; q < VE; ++q) y[q] = ys[r][col + q];
+    if (k.has_D) {
+      Raw xr[VE];
+      load16<T>(xbase + (l * k.sx[1] + col) * ES, xr);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) {
+        const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : k.Dp[hh * k.sD[0]];
+        y[q] = fmaf(Dv, M::from_raw(xr[q]), y[q]);
       }
-      if (k.has_z) {
-        if (k.out_x) Elem<T>::store(k.out_x, b * k.soutx[0] + t * k.soutx[1] + hh * k.soutx[2] + p, y);
-        const float zz = Elem<T>::load(k.z, b * k.sz[0] + t * k.sz[1] + hh * k.sz[2] + p);
-        y *= zz * sigmoidf_(zz);
-      }
-      Elem<T>::store(k.out, b * k.sout[0] + t * k.sout[1] + hh * k.sout[2] + p, y);
     }
+    Raw o[VE];
+    if (k.has_z) {
+      Raw zr[VE];
+      load16<T>((const char*)k.z + (b * k.sz[0] + t * k.sz[1] + hh * k.sz[2] + col) * ES, zr);
+      if (k.out_x) {
+#pragma unroll
+        for (int q = 0; q < VE; ++q) o[q] = M::to_raw(y[q]);
+        *reinterpret_cast<uint4*>((char*)k.out_x + (b * k.soutx[0] + t * k.soutx[1] + hh * k.soutx[2] + col) * ES) =
+            *reinterpret_cast<const uint4*>(o);
+      }
+#pragma unroll
+      for (int q = 0; q < VE; ++q) {
+        const float zz = M::from_raw(zr[q]);
+        y[q] *= zz * sigmoidf_(zz);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < VE; ++q) o[q] = M::to_raw(y[q]);
+    *reinterpret_cast<uint4*>((char*)k.out + (b * k.sout[0] + t * k.sout[1] + hh * k.sout[2] + col) * ES) =
+        *reinterpret_cast<const uint4*>(o);
   }
 }
 
