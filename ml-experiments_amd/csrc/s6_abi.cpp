@@ -392,6 +392,8 @@ int ssd_check_problem(const S6SsdProblem& p) {
     return fail(S6_E_UNSUPPORTED, "ssd: io dtype must be bf16 or fp32");
   if (ceil_div(p.seqlen, p.chunk_size) > 65535 || p.batch * p.nheads > 65535 || p.batch > 65535)
     return fail(S6_E_UNSUPPORTED, "ssd: too many chunks or batch * nheads above 65535");
+  if ((p.chunk_size / 64) * ceil_div(p.seqlen, p.chunk_size) * p.batch * p.nheads >= ((int64_t)1 << 31))
+    return fail(S6_E_UNSUPPORTED, "ssd: batch * nheads * seqlen / 64 must be below 2^31");
   if (!(p.dt_min <= p.dt_max)) return fail(S6_E_INVALID, "ssd: dt_limit must satisfy min <= max");
   return S6_OK;
 }

@@ -288,15 +288,23 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   constexpr int XC = KST * (P / VE);                       // 16-byte x chunks per stage
   constexpr int XL = (XC + kThreads - 1) / kThreads;
   constexpr int YP = P + 4;                                // y staging pitch (floats)
-  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4;
-  constexpr int SM_BYTES = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
+  constexpr int HCH = N < 128 ? N : ((ES == 4 && P == 128) ? 64 : 128);  // H columns per stage
+  constexpr int HP = HCH + 8;                              // H staging pitch, 16-byte rows
+  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
+  constexpr int SM_A = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
+  constexpr int SM_BYTES = SM_A > HS_BYTES ? SM_A : HS_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[SM_BYTES];
   __shared__ float sls[2][KST], dls[2][KST];
   Raw (*xs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
   float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
+  Raw (*hsm)[HP] = reinterpret_cast<Raw (*)[HP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lt = blockIdx.x;
-  const int64_t c = blockIdx.y, b = blockIdx.z / k.H, hh = blockIdx.z % k.H;
+  // work id -> (head fastest, row tile, chunk, batch): one (batch, chunk)'s blocks, which
+  // share its CB tile, and one head's row tiles, which share its passed state, run together
+  const int64_t wid = xcd_work_id();
+  const int64_t hh = wid % k.H;
+  const int lt = (int)((wid / k.H) % (k.Q / 64));
+  const int64_t c = (wid / (k.H * (k.Q / 64))) % k.K, b = wid / (k.H * (k.Q / 64) * k.K);
   const int64_t g = hh / k.hpg;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
@@ -340,17 +348,42 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
 #pragma unroll
   for (int i = 0; i < PT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // (a) contribution of the state entering the chunk: e^{S_l} C_l H_c^T
+  // (a) contribution of the state entering the chunk: e^{S_l} C_l H_c^T.  H (shared by the
+  // block's 4 waves) is staged through LDS in column stages of HCH with coalesced 16-byte
+  // loads; each wave's C fragments come straight from global memory.  The condition is
+  // block-uniform, so the barriers inside are too.
   if (c > 0 || k.has_init) {
     const Raw* Crow = (const Raw*)k.Cm + b * k.sC[0] + (t0 + row) * k.sC[1] + g * k.sC[2];
     const Raw* H = (const Raw*)k.hs + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+    constexpr int HC = P * (HCH / VE);
+    constexpr int HL = (HC + kThreads - 1) / kThreads;
 #pragma unroll
-    for (int n0 = 0; n0 < N; n0 += kKs) {
-      const typename M::Frag a = row < lim ? M::load_row(Crow + n0, lane) : M::zero();
+    for (int nc = 0; nc < N; nc += HCH) {
+      typename M::Frag af[HCH / kKs];
 #pragma unroll
-      for (int pt = 0; pt < PT; ++pt)
-        M::mma(acc[pt], a, M::load_row(H + (pt * 16 + (lane & 15)) * N + n0, lane));
+      for (int i = 0; i < HCH / kKs; ++i) af[i] = row < lim ? M::load_row(Crow + nc + i * kKs, lane) : M::zero();
+      u4 hv[HL];
+#pragma unroll
+      for (int i = 0; i < HL; ++i) {
+        const int e = tid + i * kThreads;
+        const int p = e / (HCH / VE), col = (e % (HCH / VE)) * VE;
+        if (e < HC) hv[i] = *reinterpret_cast<const u4*>(H + p * N + nc + col);
+      }
+      if (nc > 0) __syncthreads();  // the previous stage is consumed
+#pragma unroll
+      for (int i = 0; i < HL; ++i) {
+        const int e = tid + i * kThreads;
+        const int p = e / (HCH / VE), col = (e % (HCH / VE)) * VE;
+        if (e < HC) *reinterpret_cast<u4*>(&hsm[p][col]) = hv[i];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < HCH / kKs; ++i)
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+          M::mma(acc[pt], af[i], M::load_row(&hsm[pt * 16 + (lane & 15)][i * kKs], lane));
     }
+    __syncthreads();  // H consumed before the intra loop writes x over it
     const int32_t seq_prev = (k.has_seq && c > 0) ? seq_at(k, b, t0 - 1) : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -481,8 +514,8 @@ hipError_t ssd_prep_pn(const SsdK& k, hipStream_t st) {
 template <typename T, int P, int N>
 hipError_t ssd_scan_pn(const SsdK& k, hipStream_t st) {
   const int qt = (int)(k.Q / 64);
-  hipLaunchKernelGGL((ssd_chunk_scan<T, P, N>), dim3((unsigned)qt, (unsigned)k.K,
-                     (unsigned)(k.Bsz * k.H)), dim3(kThreads), 0, st, k);
+  hipLaunchKernelGGL((ssd_chunk_scan<T, P, N>), dim3((unsigned)(qt * k.K * k.Bsz * k.H)), dim3(kThreads),
+                     0, st, k);
   return hipGetLastError();
 }
 

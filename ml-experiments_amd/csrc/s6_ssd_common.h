@@ -14,6 +14,7 @@ namespace s6 {
 namespace ssd {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // 16 raw bytes (kept in registers)
 constexpr int kKs = 32;            // sequence steps per MFMA K step (and per LDS slice)
 constexpr int kLp = kKs + 8;       // LDS row pitch in elements: 16-byte aligned rows
 constexpr int kThreads = 256;
@@ -83,6 +84,16 @@ template <typename T>
 __device__ inline void load16(const void* p, typename Mma<T>::Raw (&r)[Mma<T>::kVe]) {
   const uint4 v = *reinterpret_cast<const uint4*>(p);
   *reinterpret_cast<uint4*>(r) = v;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.  This maps
+// the linear workgroup id to a work id so that each XCD runs one contiguous range of work
+// ids (a bijection for any grid size): blocks that share tiles -- the heads and row tiles
+// of one (batch, chunk) -- then share one L2.
+__device__ inline int64_t xcd_work_id() {
+  const int64_t n = gridDim.x, id = blockIdx.x;
+  const int64_t x = id & 7, loc = id >> 3, q = n >> 3, r = n & 7;
+  return x * q + (x < r ? x : r) + loc;
 }
 
 __device__ inline int32_t seq_at(const SsdK& k, int64_t b, int64_t t) {
