@@ -96,7 +96,9 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   __shared__ __attribute__((aligned(16))) Raw xs[NB][P][kLp];
   __shared__ __attribute__((aligned(16))) Raw bs[NB][N][kLp];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t c = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  // work id -> (head fastest, chunk, batch): the heads of one chunk share its B (C) rows
+  const int64_t wid = xcd_work_id();
+  const int64_t hh = wid % k.H, c = (wid / k.H) % k.K, b = wid / (k.H * k.K);
   const int64_t g = hh / k.hpg;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
@@ -499,7 +501,7 @@ hipError_t ssd_prep_pn(const SsdK& k, hipStream_t st) {
   hipLaunchKernelGGL((ssd_cumsum), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz), dim3(kWave),
                      0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 0>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 0>), dim3((unsigned)(k.K * k.H * k.Bsz)),
                      dim3(kThreads), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_state_pass<T>), dim3((unsigned)((P * N + kThreads - 1) / kThreads),
@@ -521,7 +523,7 @@ hipError_t ssd_scan_pn(const SsdK& k, hipStream_t st) {
 
 template <typename T, int P, int N>
 hipError_t ssd_dstates_pn(const SsdK& k, hipStream_t st) {
-  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 1>), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz),
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 1>), dim3((unsigned)(k.K * k.H * k.Bsz)),
                      dim3(kThreads), 0, st, k);
   return hipGetLastError();
 }

@@ -126,8 +126,11 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   __shared__ float sls[kKs];
   __shared__ float dred[kThreads / kWave][P];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lt = blockIdx.x;
-  const int64_t c = blockIdx.y, b = blockIdx.z / k.H, hh = blockIdx.z % k.H;
+  // work id -> (head fastest, row tile, chunk, batch), as the chunk scan
+  const int64_t wid = xcd_work_id();
+  const int64_t hh = wid % k.H;
+  const int lt = (int)((wid / k.H) % (k.Q / 64));
+  const int64_t c = (wid / (k.H * (k.Q / 64))) % k.K, b = wid / (k.H * (k.Q / 64) * k.K);
   const int64_t g = hh / k.hpg;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
@@ -268,8 +271,9 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
   constexpr int ES = sizeof(Raw);
   __shared__ __attribute__((aligned(16))) Raw ms[N][kLp];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lt = blockIdx.x;
-  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
+  const int lt = (int)(wid % (k.Q / 64));
+  const int64_t c = (wid / (k.Q / 64)) % k.K, b = wid / ((k.Q / 64) * k.K * k.G), g = (wid / ((k.Q / 64) * k.K)) % k.G;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
   if (lt * 64 >= lim) return;
@@ -346,8 +350,9 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dcb(SsdK k) {
   typedef typename M::Raw Raw;
   __shared__ float csred[kThreads / kWave][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int I = blockIdx.x;
-  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
+  const int I = (int)(wid % (k.Q / 64));
+  const int64_t c = (wid / (k.Q / 64)) % k.K, b = wid / ((k.Q / 64) * k.K * k.G), g = (wid / ((k.Q / 64) * k.K)) % k.G;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
   if (I * 64 >= lim) return;
@@ -451,8 +456,9 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
   constexpr int ES = sizeof(Raw);
   __shared__ __attribute__((aligned(16))) Raw os[N][kLp];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lt = blockIdx.x;
-  const int64_t c = blockIdx.y, b = blockIdx.z / k.G, g = blockIdx.z % k.G;
+  const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
+  const int lt = (int)(wid % (k.Q / 64));
+  const int64_t c = (wid / (k.Q / 64)) % k.K, b = wid / ((k.Q / 64) * k.K * k.G), g = (wid / ((k.Q / 64) * k.K)) % k.G;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
   if (lt * 64 >= lim) return;
@@ -631,22 +637,22 @@ hipError_t ssd_bwd_pn(const SsdK& k, hipStream_t st) {
   if ((e = launch_ssd_dstates(k, st)) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_state_pass_bwd<T>), dim3((unsigned)k.nE, (unsigned)k.H, (unsigned)k.Bsz), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_dx<T, P, N>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.H)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_dx<T, P, N>), dim3((unsigned)(qt * k.K * k.Bsz * k.H)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 4>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 4>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   switch (qt) {
-    case 1: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 1>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
-    case 2: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 2>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
-    case 4: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 4>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k); break;
+    case 1: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 1>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
+    case 2: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 2>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
+    case 4: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 4>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
     default: return hipErrorInvalidValue;
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 0>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 0>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 1>), dim3(qt, (unsigned)k.K, (unsigned)(k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 1>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_dt), dim3((unsigned)k.K, (unsigned)k.H, (unsigned)k.Bsz), dim3(kWave), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
