@@ -364,7 +364,7 @@ SsdPlan ssd_plan(const S6SsdProblem& p) {
   s.off_dDp = off; off += align256((size_t)(p.batch * s.K * qt * p.nheads * p.headdim) * 4);
   s.off_qv = off; off += align256(bhkq);
   s.off_uv = off; off += align256(bhkq);
-  s.off_rs = off; off += align256(bhkq);
+  s.off_rs = off; off += align256(bhkq * (size_t)qt);  // one partial per column tile
   s.off_csp = off; off += align256(bhkq * (size_t)qt);
   const size_t lgn = (size_t)(p.batch * p.seqlen * p.ngroups * p.dstate) * 4;
   s.off_dBp = off; off += align256(lgn);

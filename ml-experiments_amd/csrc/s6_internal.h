@@ -173,7 +173,7 @@ struct SsdK {
   float* dBp;     // [Bsz, L, G, N] fp32 dB from the chunk states
   float* dCp;     // [Bsz, L, G, N] fp32 dC from the entering states
   float* dcb;     // [Bsz, K, G, Q, Q] gradient of C B^T (lower-triangle tiles)
-  float* rs;      // [Bsz, H, K, Q] row sums of the intra-chunk decay terms
+  float* rs;      // [Q/64, Bsz, H, K, Q] row sums of the intra-chunk decay terms, per column tile
   float* csp;     // [Bsz, H, K, Q/64, Q] column-sum partials per row tile
   float* dAp;     // [Bsz * K, H] partial dA
   float* dbp;     // [Bsz * K, H] partial ddt_bias

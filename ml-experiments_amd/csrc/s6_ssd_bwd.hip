@@ -14,7 +14,7 @@
 //   ssd_bwd_rows<4>    dB_s += sum_h mlast dt'_s e^{S_last-S_s} x_s^h dst^h; q_s per head MFMA
 //   ssd_bwd_rows<5>    dC_l += sum_h mprev e^{S_l} G_l^h H^h;             u_l per head  MFMA
 //   ssd_bwd_dcb        dM = G x^T per head; dCB = sum_h dM e^{S_l-S_s} dt'_s; row / column
-//                      sums of W = dM CB e^{S_l-S_s} dt'_s                             MFMA
+//                      sums of W = dM CB e^{S_l-S_s} dt'_s, one block per 64x64 tile   MFMA
 //   ssd_bwd_bmm<C|B>   dC += dCB B, dB += dCB^T C                                     MFMA
 //   ssd_bwd_dt         dS = u + rowsum(W) - colsum(W) - q (+ the S_last terms at the chunk
 //                      end); da = reverse cumsum of dS; ddt = A da + ddt'; through clamp,
@@ -344,103 +344,160 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
 
 // ---- dCB and the intra-chunk decay terms ---------------------------------------------
 
-template <typename T, int P, int QT>
+// Block: one 64x64 tile (I, J), J <= I, of dCB for one chunk and group; it loops over the
+// group's heads.  Per head, dM = G_I X_J^T on MFMA, with the x tile staged untransposed in
+// LDS (its rows are the B operand's K-contiguous rows) and each wave's dy rows straight from
+// global memory; then, elementwise, dCB += dM e^{S_l - S_s} dt'_s and W = that times CB, whose
+// row sums (per tile J: partials summed by ssd_bwd_dt) and column sums (reduced over the
+// block's waves in LDS) feed the dt gradient.  The next head's x tile, dy fragments and
+// cumsums are loaded while the current head computes; CB's values at this lane's
+// accumulator positions do not depend on the head and stay in registers.
+template <typename T, int P>
 __global__ void __launch_bounds__(kThreads) ssd_bwd_dcb(SsdK k) {
   typedef Mma<T> M;
   typedef typename M::Raw Raw;
-  __shared__ float csred[kThreads / kWave][64];
+  typedef typename M::Frag Frag;
+  constexpr int VE = M::kVe;
+  constexpr int XP = P + 8;                 // x tile pitch, 16-byte rows
+  constexpr int XC = 64 * (P / VE);         // 16-byte chunks per x tile
+  constexpr int XL = (XC + kThreads - 1) / kThreads;
+  constexpr int KF = P / kKs;               // MFMA K steps over headdim
+  __shared__ __attribute__((aligned(16))) Raw xs[2][64][XP];
+  __shared__ float csred[2][kThreads / kWave][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
-  const int I = (int)(wid % (k.Q / 64));
-  const int64_t c = (wid / (k.Q / 64)) % k.K, b = wid / ((k.Q / 64) * k.K * k.G), g = (wid / ((k.Q / 64) * k.K)) % k.G;
+  const int QT = (int)(k.Q / 64);
+  const int64_t ntile = QT * (QT + 1) / 2;
+  const int64_t wid = xcd_work_id();  // (tile fastest, chunk, batch * group)
+  int I = 0, J = (int)(wid % ntile);
+  while (J > I) { J -= I + 1; ++I; }
+  const int64_t c = (wid / ntile) % k.K, bg = wid / (ntile * k.K);
+  const int64_t b = bg / k.G, g = bg % k.G;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
-  if (I * 64 >= lim) return;
+  if (I * 64 >= lim) return;  // whole block (J <= I)
   const int rowbase = I * 64 + 16 * w;
   const int row = rowbase + (lane & 15);
   const float* cbm = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
-  f4 dcb[QT][4];
+  const int64_t nrs = k.Bsz * k.H * k.K * k.Q;  // elements of one row-sum partial
+  float cbv[4][4];
 #pragma unroll
-  for (int J = 0; J < QT; ++J)
+  for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) dcb[J][ct] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t hh = g * k.hpg; hh < (g + 1) * k.hpg; ++hh) {
-    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
-    const float* sq = k.dacs + hrow;
-    const float* dq = k.dtq + hrow;
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j, s = J * 64 + ct * 16 + (lane & 15);
+      cbv[ct][j] = (l < lim && s < lim) ? cbm[(int64_t)l * k.Q + s] : 0.f;
+    }
+  f4 dcb[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) dcb[ct] = f4{0.f, 0.f, 0.f, 0.f};
+
+  Raw xv[XL][VE];
+  Frag gf[KF];
+  float slv[4], ssv[4], dsv[4];
+  auto fetch = [&](int64_t hh) {
+    const char* xb = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * sizeof(Raw);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      const int s = J * 64 + r;
+      if (e < XC && s < lim) load16<T>(xb + (s * k.sx[1] + col) * sizeof(Raw), xv[i]);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) xv[i][q] = M::to_raw(0.f);
+    }
     const Raw* grow = (const Raw*)k.dy + b * k.sdy[0] + (t0 + row) * k.sdy[1] + hh * k.sdy[2];
-    const Raw* xb = (const Raw*)k.x + b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2];
-    float sl[4], rsum[4];
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk) gf[kk] = row < lim ? M::load_row(grow + kk * kKs, lane) : M::zero();
+    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j;
-      sl[j] = l < lim ? sq[l] : 0.f;
-      rsum[j] = 0.f;
+      slv[j] = l < lim ? k.dacs[hrow + l] : 0.f;
     }
 #pragma unroll
-    for (int J = 0; J < QT; ++J) {
-      if (J > I) break;  // block-uniform
-      f4 dM[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) dM[ct] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p0 = 0; p0 < P; p0 += kKs) {
-        const typename M::Frag a = row < lim ? M::load_row(grow + p0, lane) : M::zero();
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int s = J * 64 + ct * 16 + (lane & 15);
-          const typename M::Frag bf = s < lim ? M::load_row(xb + s * k.sx[1] + p0, lane) : M::zero();
-          M::mma(dM[ct], a, bf);
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int s = J * 64 + ct * 16 + (lane & 15);
-        const float ssv = sq[s], dsv = dq[s];
-        float colsum = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int l = rowbase + 4 * (lane >> 4) + j;
-          const bool on = s <= l && l < lim && s < lim;
-          const float ev = exp_split(sl[j] - ssv);
-          const float dme = on ? dM[ct][j] * ev * dsv : 0.f;
-          dcb[J][ct][j] += dme;
-          const float wv = dme * cbm[(int64_t)l * k.Q + s];
-          rsum[j] += wv;
-          colsum += wv;
-        }
-        colsum += __shfl_xor(colsum, 16);
-        colsum += __shfl_xor(colsum, 32);
-        if (lane < 16) csred[w][ct * 16 + lane] = colsum;
-      }
-      __syncthreads();
-      if (tid < 64)
-        k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + J * 64 + tid] =
-            csred[0][tid] + csred[1][tid] + csred[2][tid] + csred[3][tid];
-      __syncthreads();
+    for (int ct = 0; ct < 4; ++ct) {
+      const int s = J * 64 + ct * 16 + (lane & 15);  // < Q: rows past lim hold dt' = 0
+      ssv[ct] = k.dacs[hrow + s];
+      dsv[ct] = k.dtq[hrow + s];
     }
+  };
+  auto write_csp = [&](int64_t hh, int buf) {
+    k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + J * 64 + tid] =
+        csred[buf][0][tid] + csred[buf][1][tid] + csred[buf][2][tid] + csred[buf][3][tid];
+  };
+
+  const int64_t h0 = g * k.hpg;
+  fetch(h0);
+  for (int hi = 0; hi < (int)k.hpg; ++hi) {
+    const int buf = hi & 1;
+    const int64_t hh = h0 + hi;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < XC) {
+        const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+        *reinterpret_cast<u4*>(&xs[buf][r][col]) = *reinterpret_cast<const u4*>(xv[i]);
+      }
+    }
+    Frag gc[KF];
+    float slc[4], ssc[4], dsc[4];
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk) gc[kk] = gf[kk];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { slc[j] = slv[j]; ssc[j] = ssv[j]; dsc[j] = dsv[j]; }
+    __syncthreads();
+    if (hi > 0 && tid < 64) write_csp(hh - 1, buf ^ 1);
+    if (hi + 1 < (int)k.hpg) fetch(hh + 1);
+    f4 dM[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) dM[ct] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        M::mma(dM[ct], gc[kk], M::load_row(&xs[buf][ct * 16 + (lane & 15)][kk * kKs], lane));
+    float rsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int s = J * 64 + ct * 16 + (lane & 15);
+      float colsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int l = rowbase + 4 * (lane >> 4) + j;
+        const bool on = s <= l && l < lim && s < lim;
+        const float dme = on ? dM[ct][j] * exp_split(slc[j] - ssc[ct]) * dsc[ct] : 0.f;
+        dcb[ct][j] += dme;
+        const float wv = dme * cbv[ct][j];
+        rsum[j] += wv;
+        colsum += wv;
+      }
+      colsum += __shfl_xor(colsum, 16);
+      colsum += __shfl_xor(colsum, 32);
+      if (lane < 16) csred[buf][w][ct * 16 + lane] = colsum;
+    }
+    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j;
       const float v = wave_sum16(rsum[j]);
-      if ((lane & 15) == 0 && l < lim) k.rs[hrow + l] = v;
+      if ((lane & 15) == 0 && l < lim) k.rs[J * nrs + hrow + l] = v;
     }
   }
+  __syncthreads();
+  if (tid < 64) write_csp(h0 + k.hpg - 1, (int)((k.hpg - 1) & 1));
+
   float* out = k.dcb + ((b * k.K + c) * k.G + g) * k.Q * k.Q;
 #pragma unroll
-  for (int J = 0; J < QT; ++J) {
-    if (J > I) break;
+  for (int ct = 0; ct < 4; ++ct) {
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int l = rowbase + 4 * (lane >> 4) + j;
-        const int s = J * 64 + ct * 16 + (lane & 15);
-        float v = dcb[J][ct][j];
-        if (!(l < lim && s < lim)) v = 0.f;
-        else if (k.has_seq && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
-        out[(int64_t)l * k.Q + s] = v;
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      const int s = J * 64 + ct * 16 + (lane & 15);
+      float v = dcb[ct][j];
+      if (!(l < lim && s < lim)) v = 0.f;
+      else if (k.has_seq && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
+      out[(int64_t)l * k.Q + s] = v;
     }
   }
 }
@@ -528,6 +585,7 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
   const int lim = (int)min(k.Q, k.L - t0);
   const int QT = (int)(k.Q / 64);
   const int nI = (lim + 63) / 64;  // row tiles that ran
+  const int64_t nrs = k.Bsz * k.H * k.K * k.Q;
   float ddal = 0.f;
   for (int64_t e = lane; e < k.nE; e += kWave) ddal += k.ddal[((b * k.H + hh) * k.K + c) * k.nE + e];
   float qv[4], dS[4];
@@ -551,7 +609,9 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
     if (j < lim) {
       float cs = 0.f;
       for (int I = j / 64; I < nI; ++I) cs += k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + j];
-      d += k.uv[hrow + j] + k.rs[hrow + j] - cs - qv[q];
+      float rsj = 0.f;  // row sum: one partial per column tile J <= j / 64
+      for (int J = 0; J <= j / 64; ++J) rsj += k.rs[J * nrs + hrow + j];
+      d += k.uv[hrow + j] + rsj - cs - qv[q];
     }
     dS[q] = d;
     tot += d;
@@ -643,12 +703,7 @@ hipError_t ssd_bwd_pn(const SsdK& k, hipStream_t st) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  switch (qt) {
-    case 1: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 1>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
-    case 2: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 2>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
-    case 4: hipLaunchKernelGGL((ssd_bwd_dcb<T, P, 4>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k); break;
-    default: return hipErrorInvalidValue;
-  }
+  hipLaunchKernelGGL((ssd_bwd_dcb<T, P>), dim3((unsigned)(qt * (qt + 1) / 2 * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_bmm<T, N, 0>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
