@@ -362,8 +362,9 @@ SsdPlan ssd_plan(const S6SsdProblem& p) {
   s.off_ddal = off; off += align256((size_t)(p.batch * p.nheads * s.K * s.nE) * 4);
   s.off_ddtd = off; off += align256(bhkq);
   s.off_dDp = off; off += align256((size_t)(p.batch * s.K * qt * p.nheads * p.headdim) * 4);
-  s.off_qv = off; off += align256(bhkq);
-  s.off_uv = off; off += align256(bhkq);
+  const size_t nsl = (size_t)(p.dstate / (p.dstate < 64 ? p.dstate : 64));  // dstate slices of the row kernels
+  s.off_qv = off; off += align256(bhkq * nsl);
+  s.off_uv = off; off += align256(bhkq * nsl);
   s.off_rs = off; off += align256(bhkq * (size_t)qt);  // one partial per column tile
   s.off_csp = off; off += align256(bhkq * (size_t)qt);
   const size_t lgn = (size_t)(p.batch * p.seqlen * p.ngroups * p.dstate) * 4;

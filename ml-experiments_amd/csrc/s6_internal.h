@@ -168,8 +168,8 @@ struct SsdK {
   int64_t nE;     // element blocks of the state passing backward
   float* ddtd;    // [Bsz, H, K, Q] direct dt gradient (x . (T1 + T2))
   float* dDp;     // [Bsz * K * Q/64, H(, P)] partial dD
-  float* qv;      // [Bsz, H, K, Q] chunk-state decay terms
-  float* uv;      // [Bsz, H, K, Q] inter-chunk decay terms
+  float* qv;      // [N / min(N, 64), Bsz, H, K, Q] chunk-state decay terms, per dstate slice
+  float* uv;      // [N / min(N, 64), Bsz, H, K, Q] inter-chunk decay terms, per dstate slice
   float* dBp;     // [Bsz, L, G, N] fp32 dB from the chunk states
   float* dCp;     // [Bsz, L, G, N] fp32 dC from the entering states
   float* dcb;     // [Bsz, K, G, Q, Q] gradient of C B^T (lower-triangle tiles)

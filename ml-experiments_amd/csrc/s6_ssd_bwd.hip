@@ -262,18 +262,35 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
 // ---- per-group row products: dB from the chunk states (MODE 4), dC from the entering
 // states (MODE 5) ------------------------------------------------------------------------
 
+// Block: 64 rows of one chunk and group and a slice of NC dstate columns; it loops over the
+// group's heads, accumulating f_h(l) A_h[l, :] mat_h[:, n] (A = x, mat = dst for dB; A = dy,
+// mat = H for dC) and writing the per-head row sums against B (C) as one partial per column
+// slice.  The next head's matrix slice, A fragments and cumsums are loaded while the current
+// head computes; the matrix goes transposed (dstate-major, K = headdim contiguous) into a
+// double LDS buffer written with lanes along headdim, so the 2-byte writes do not collide.
 template <typename T, int P, int N, int MODE>
 __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
   typedef Mma<T> M;
   typedef typename M::Raw Raw;
+  typedef typename M::Frag Frag;
   constexpr int VE = M::kVe;
-  constexpr int NT = N / 16;
   constexpr int ES = sizeof(Raw);
-  __shared__ __attribute__((aligned(16))) Raw ms[N][kLp];
+  constexpr int NC = N < 64 ? N : 64;       // dstate columns per block
+  constexpr int NS = N / NC;
+  constexpr int NT = NC / 16;
+  constexpr int MP = P + 8;                 // LDS pitch, 16-byte rows
+  constexpr int NB = 2 * NC * MP * ES <= 40960 ? 2 : 1;
+  constexpr int MC = P * (NC / VE);         // 16-byte chunks of one head's matrix slice
+  constexpr int ML = (MC + kThreads - 1) / kThreads;
+  constexpr int KF = P / kKs;
+  __shared__ __attribute__((aligned(16))) Raw ms[NB][NC][MP];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
-  const int lt = (int)(wid % (k.Q / 64));
-  const int64_t c = (wid / (k.Q / 64)) % k.K, b = wid / ((k.Q / 64) * k.K * k.G), g = (wid / ((k.Q / 64) * k.K)) % k.G;
+  const int QT = (int)(k.Q / 64);
+  const int64_t wid = xcd_work_id();  // (column slice fastest, row tile, chunk, batch * group)
+  const int ns = (int)(wid % NS);
+  const int lt = (int)((wid / NS) % QT);
+  const int64_t c = (wid / (NS * QT)) % k.K, bg = wid / (NS * QT * k.K);
+  const int64_t b = bg / k.G, g = bg % k.G;
   const int64_t t0 = c * k.Q;
   const int lim = (int)min(k.Q, k.L - t0);
   if (lt * 64 >= lim) return;
@@ -281,54 +298,96 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
   const int row = rowbase + (lane & 15);
   const int64_t* sa = MODE == 4 ? k.sx : k.sdy;
   const Raw* abase = (const Raw*)(MODE == 4 ? k.x : k.dy) + b * sa[0] + (t0 + row) * sa[1];
-  const Raw* side = (const Raw*)(MODE == 4 ? k.Bm : k.Cm);
+  const void* side = MODE == 4 ? k.Bm : k.Cm;
   const int64_t* ss = MODE == 4 ? k.sB : k.sC;
   const int32_t seq_ref = !k.has_seq ? 0
                           : MODE == 4 ? seq_last_of(k, b, c) : (c > 0 ? seq_at(k, b, t0 - 1) : 0);
+  const int64_t nrs = k.Bsz * k.H * k.K * k.Q;
+  // head-independent: row masks and B (C) at this lane's accumulator positions
+  bool rv[4];
+  float sd[4][NT];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = rowbase + 4 * (lane >> 4) + j;
+    rv[j] = l < lim && (!k.has_seq || seq_at(k, b, t0 + l) == seq_ref);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      sd[j][nt] = l < lim ? Elem<T>::load(side, b * ss[0] + (t0 + l) * ss[1] + g * ss[2] + ns * NC + nt * 16 + (lane & 15))
+                          : 0.f;
+  }
   f4 tot[NT];
 #pragma unroll
   for (int i = 0; i < NT; ++i) tot[i] = f4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t hh = g * k.hpg; hh < (g + 1) * k.hpg; ++hh) {
+
+  Raw mv[ML][VE];
+  Frag af[KF];
+  float sqv[4], dqv[4], slv = 0.f;
+  auto fetch = [&](int64_t hh) {
     const Raw* mat = (const Raw*)(MODE == 4 ? k.dst : k.hs) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
-    f4 acc[NT];
 #pragma unroll
-    for (int i = 0; i < NT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < P; p0 += kKs) {
-      __syncthreads();
-      for (int e = tid; e < kKs * (N / VE); e += kThreads) {  // mat rows p0..p0+31 -> ms[n][p]
-        const int r = e / (N / VE), col = (e % (N / VE)) * VE;
-        Raw v[VE];
-        load16<T>(mat + (p0 + r) * N + col, v);
-#pragma unroll
-        for (int q = 0; q < VE; ++q) ms[col + q][r] = v[q];
-      }
-      __syncthreads();
-      const typename M::Frag a = row < lim ? M::load_row(abase + hh * sa[2] + p0, lane) : M::zero();
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) M::mma(acc[nt], a, M::load_row(&ms[nt * 16 + (lane & 15)][0], lane));
+    for (int i = 0; i < ML; ++i) {
+      const int e = tid + i * kThreads;
+      const int p = e % P, n0 = (e / P) * VE;
+      if (e < MC) load16<T>(mat + p * N + ns * NC + n0, mv[i]);
     }
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk) af[kk] = row < lim ? M::load_row(abase + hh * sa[2] + kk * kKs, lane) : M::zero();
     const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
-    const float* sq = k.dacs + hrow;
-    const float* dq = k.dtq + hrow;
-    const float s_last = sq[k.Q - 1];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j;
-      float f = 0.f;
-      if (l < lim) {
-        f = MODE == 4 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
-        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) f = 0.f;
+      sqv[j] = l < lim ? k.dacs[hrow + l] : 0.f;
+      dqv[j] = (MODE == 4 && l < lim) ? k.dtq[hrow + l] : 0.f;
+    }
+    if (MODE == 4) slv = k.dacs[hrow + k.Q - 1];
+  };
+
+  const int64_t h0 = g * k.hpg;
+  fetch(h0);
+  for (int hi = 0; hi < (int)k.hpg; ++hi) {
+    const int buf = NB == 2 ? (hi & 1) : 0;
+    const int64_t hh = h0 + hi;
+    if (NB == 1 && hi > 0) __syncthreads();  // the single buffer is consumed
+#pragma unroll
+    for (int i = 0; i < ML; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < MC) {
+        const int p = e % P, n0 = (e / P) * VE;
+#pragma unroll
+        for (int q = 0; q < VE; ++q) ms[buf][n0 + q][p] = mv[i][q];
       }
+    }
+    Frag ac[KF];
+    float sqc[4], dqc[4];
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk) ac[kk] = af[kk];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { sqc[j] = sqv[j]; dqc[j] = dqv[j]; }
+    const float slc = slv;
+    __syncthreads();
+    if (hi + 1 < (int)k.hpg) fetch(hh + 1);
+    f4 acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KF; ++kk)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        M::mma(acc[nt], ac[kk], M::load_row(&ms[buf][nt * 16 + (lane & 15)][kk * kKs], lane));
+    const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int l = rowbase + 4 * (lane >> 4) + j;
+      const float f = !rv[j] ? 0.f : MODE == 4 ? dqc[j] * exp_split(slc - sqc[j]) : exp_split(sqc[j]);
       float sv = 0.f;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        acc[nt][j] *= f;
-        const float sd = l < lim ? Elem<T>::load(side, b * ss[0] + (t0 + l) * ss[1] + g * ss[2] + nt * 16 + (lane & 15)) : 0.f;
-        sv = fmaf(sd, acc[nt][j], sv);
-        tot[nt][j] += acc[nt][j];
+        const float a = acc[nt][j] * f;
+        sv = fmaf(sd[j][nt], a, sv);
+        tot[nt][j] += a;
       }
       sv = wave_sum16(sv);
-      if ((lane & 15) == 0 && l < lim) (MODE == 4 ? k.qv : k.uv)[hrow + l] = sv;
+      if ((lane & 15) == 0 && l < lim) (MODE == 4 ? k.qv : k.uv)[ns * nrs + hrow + l] = sv;
     }
   }
   float* outp = MODE == 4 ? k.dBp : k.dCp;
@@ -338,7 +397,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
     if (l >= lim) continue;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-      outp[((b * k.L + t0 + l) * k.G + g) * N + nt * 16 + (lane & 15)] = tot[nt][j];
+      outp[((b * k.L + t0 + l) * k.G + g) * N + ns * NC + nt * 16 + (lane & 15)] = tot[nt][j];
   }
 }
 
@@ -590,10 +649,13 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
   for (int64_t e = lane; e < k.nE; e += kWave) ddal += k.ddal[((b * k.H + hh) * k.K + c) * k.nE + e];
   float qv[4], dS[4];
   float qsum = 0.f;
+  const int nsl = (int)(k.N / (k.N < 64 ? k.N : 64));  // dstate column slices of ssd_bwd_rows
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int j = 4 * lane + q;
-    qv[q] = j < lim ? k.qv[hrow + j] : 0.f;
+    qv[q] = 0.f;
+    if (j < lim)
+      for (int i = 0; i < nsl; ++i) qv[q] += k.qv[i * nrs + hrow + j];
     qsum += qv[q];
   }
 #pragma unroll
@@ -611,7 +673,9 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_dt(SsdK k) {
       for (int I = j / 64; I < nI; ++I) cs += k.csp[(((b * k.H + hh) * k.K + c) * QT + I) * k.Q + j];
       float rsj = 0.f;  // row sum: one partial per column tile J <= j / 64
       for (int J = 0; J <= j / 64; ++J) rsj += k.rs[J * nrs + hrow + j];
-      d += k.uv[hrow + j] + rsj - cs - qv[q];
+      float uvj = 0.f;
+      for (int i = 0; i < nsl; ++i) uvj += k.uv[i * nrs + hrow + j];
+      d += uvj + rsj - cs - qv[q];
     }
     dS[q] = d;
     tot += d;
@@ -699,9 +763,9 @@ hipError_t ssd_bwd_pn(const SsdK& k, hipStream_t st) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_dx<T, P, N>), dim3((unsigned)(qt * k.K * k.Bsz * k.H)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 4>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 4>), dim3((unsigned)(N / (N < 64 ? N : 64) * qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3((unsigned)(qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
+  hipLaunchKernelGGL((ssd_bwd_rows<T, P, N, 5>), dim3((unsigned)(N / (N < 64 ? N : 64) * qt * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_dcb<T, P>), dim3((unsigned)(qt * (qt + 1) / 2 * k.K * k.Bsz * k.G)), blk, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
