@@ -115,6 +115,12 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_bwd(SsdK k) {
 
 // ---- dx, direct dt gradient, dD parts ------------------------------------------------
 
+// Block: 64 rows (steps s) of one chunk and head, 4 waves of 16 rows, all of headdim; the
+// layout of the forward's chunk scan.  T2 stages dst through LDS in column stages; T1 runs
+// as a software pipeline over stages of SUB MFMA K steps (l >= s): the dy rows and this
+// wave's CB column values of stage i + 1 are loaded while stage i computes, dy goes
+// transposed into a double LDS buffer, one barrier per stage.  The epilogue stages
+// T1 + T2 through LDS so that x, dy and dx move as 16-byte rows.
 template <typename T, int P, int N>
 __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   typedef Mma<T> M;
@@ -122,9 +128,24 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   constexpr int VE = M::kVe;
   constexpr int PT = P / 16;
   constexpr int ES = sizeof(Raw);
-  __shared__ __attribute__((aligned(16))) Raw gs[P][kLp];
-  __shared__ float sls[kKs];
+  constexpr int SUB = (ES == 2 || P <= 64) ? 2 : 1;       // MFMA K steps per stage
+  constexpr int KST = SUB * kKs;                           // steps per stage
+  constexpr int LP = KST + 8;                              // LDS row pitch, 16-byte rows
+  constexpr int XC = KST * (P / VE);                       // 16-byte dy chunks per stage
+  constexpr int XL = (XC + kThreads - 1) / kThreads;
+  constexpr int YP = P + 4;                                // T staging pitch (floats)
+  constexpr int HCH = N < 128 ? N : ((ES == 4 && P == 128) ? 64 : 128);  // dst columns per stage
+  constexpr int HP = HCH + 8;
+  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
+  constexpr int SM_A = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
+  constexpr int SM_BYTES = SM_A > HS_BYTES ? SM_A : HS_BYTES;
+  constexpr int RPT = P / VE;                              // threads per row in the epilogue
+  __shared__ __attribute__((aligned(16))) char smem[SM_BYTES];
+  __shared__ float sls[2][KST];
   __shared__ float dred[kThreads / kWave][P];
+  Raw (*gs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
+  float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
+  Raw (*dsm)[HP] = reinterpret_cast<Raw (*)[HP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // work id -> (head fastest, row tile, chunk, batch), as the chunk scan
   const int64_t wid = xcd_work_id();
@@ -140,21 +161,73 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   const float* dq = k.dtq + hrow;
   const int rowbase = lt * 64 + 16 * w;
   const int row = rowbase + (lane & 15);
+  const float* cbcol = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + row;
+  const char* gbase = (const char*)k.dy + (b * k.sdy[0] + t0 * k.sdy[1] + hh * k.sdy[2]) * ES;
+  const int nst = (lim - lt * 64 + KST - 1) / KST;
+
+  Raw gv[XL][VE];
+  float cbv[SUB][8];
+  float sv = 0.f;
+  auto fetch = [&](int l0) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+      if (e < XC && l0 + r < lim) load16<T>(gbase + ((l0 + r) * k.sdy[1] + col) * ES, gv[i]);
+      else
+#pragma unroll
+        for (int q = 0; q < VE; ++q) gv[i][q] = M::to_raw(0.f);
+    }
+    if (tid < KST) sv = l0 + tid < k.Q ? sq[l0 + tid] : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks) {
+      const bool reach = l0 + ks * kKs + kKs - 1 >= rowbase;  // wave-uniform
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int l = l0 + ks * kKs + M::kidx(lane, j);
+        cbv[ks][j] = (reach && l < lim) ? cbcol[(int64_t)l * k.Q] : 0.f;
+      }
+    }
+  };
+  fetch(lt * 64);
+
   f4 acc[PT];
 #pragma unroll
   for (int i = 0; i < PT; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // T2: B_s dst^T, rows scaled by mlast e^{S_last - S_s}
+  // T2: B_s dst^T, rows scaled by mlast e^{S_last - S_s}; dst staged through LDS
   {
     const Raw* Brow = (const Raw*)k.Bm + b * k.sB[0] + (t0 + row) * k.sB[1] + g * k.sB[2];
     const Raw* D2 = (const Raw*)k.dst + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+    constexpr int HC = P * (HCH / VE);
+    constexpr int HL = (HC + kThreads - 1) / kThreads;
 #pragma unroll
-    for (int n0 = 0; n0 < N; n0 += kKs) {
-      const typename M::Frag a = row < lim ? M::load_row(Brow + n0, lane) : M::zero();
+    for (int nc = 0; nc < N; nc += HCH) {
+      typename M::Frag af[HCH / kKs];
 #pragma unroll
-      for (int pt = 0; pt < PT; ++pt)
-        M::mma(acc[pt], a, M::load_row(D2 + (pt * 16 + (lane & 15)) * N + n0, lane));
+      for (int i = 0; i < HCH / kKs; ++i) af[i] = row < lim ? M::load_row(Brow + nc + i * kKs, lane) : M::zero();
+      u4 hv[HL];
+#pragma unroll
+      for (int i = 0; i < HL; ++i) {
+        const int e = tid + i * kThreads;
+        const int p = e / (HCH / VE), col = (e % (HCH / VE)) * VE;
+        if (e < HC) hv[i] = *reinterpret_cast<const u4*>(D2 + p * N + nc + col);
+      }
+      if (nc > 0) __syncthreads();
+#pragma unroll
+      for (int i = 0; i < HL; ++i) {
+        const int e = tid + i * kThreads;
+        const int p = e / (HCH / VE), col = (e % (HCH / VE)) * VE;
+        if (e < HC) *reinterpret_cast<u4*>(&dsm[p][col]) = hv[i];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < HCH / kKs; ++i)
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+          M::mma(acc[pt], af[i], M::load_row(&dsm[pt * 16 + (lane & 15)][i * kKs], lane));
     }
+    __syncthreads();  // dst consumed before the T1 loop writes dy over it
     const float s_last = sq[k.Q - 1];
     const int32_t seq_last = k.has_seq ? seq_last_of(k, b, c) : 0;
 #pragma unroll
@@ -172,78 +245,104 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
 
   // T1: sum_{l >= s} CB[l, s] e^{S_l - S_s} G_l
   const float s_row = row < lim ? sq[row] : 0.f;
-  const float* cbcol = k.cb + ((b * k.K + c) * k.G + g) * k.Q * k.Q + row;
-  const char* gbase = (const char*)k.dy + (b * k.sdy[0] + t0 * k.sdy[1] + hh * k.sdy[2]) * ES;
-  for (int l0 = lt * 64; l0 < lim; l0 += kKs) {
-    __syncthreads();
-    for (int e = tid; e < kKs * (P / VE); e += kThreads) {
-      const int r = e / (P / VE), col = (e % (P / VE)) * VE;
-      Raw v[VE];
-      if (l0 + r < lim) load16<T>(gbase + ((l0 + r) * k.sdy[1] + col) * ES, v);
-      else
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const int l0 = lt * 64 + st * KST;
 #pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+    for (int i = 0; i < XL; ++i) {
+      const int e = tid + i * kThreads;
+      if (e < XC) {
+        const int r = e / (P / VE), col = (e % (P / VE)) * VE;
 #pragma unroll
-      for (int q = 0; q < VE; ++q) gs[col + q][r] = v[q];
-    }
-    if (tid < kKs) sls[tid] = sq[l0 + tid];
-    __syncthreads();
-    if (l0 + kKs - 1 >= rowbase) {  // wave-uniform
-      float m[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int li = M::kidx(lane, j);
-        const int l = l0 + li;
-        const bool on = l >= row && l < lim && row < lim;
-        const float v = cbcol[(int64_t)l * k.Q] * exp_split(sls[li] - s_row);
-        m[j] = on ? v : 0.f;
+        for (int q = 0; q < VE; ++q) gs[buf][col + q][r] = gv[i][q];
       }
-      const typename M::Frag a = M::from_float(m);
+    }
+    if (tid < KST) sls[buf][tid] = sv;
+    float cbc[SUB][8];
 #pragma unroll
-      for (int pt = 0; pt < PT; ++pt)
-        M::mma(acc[pt], a, M::load_row(&gs[pt * 16 + (lane & 15)][0], lane));
+    for (int ks = 0; ks < SUB; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cbc[ks][j] = cbv[ks][j];
+    __syncthreads();
+    if (st + 1 < nst) fetch(l0 + KST);
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks) {
+      if (l0 + ks * kKs + kKs - 1 >= rowbase) {  // wave-uniform: the slice reaches this wave's rows
+        float m[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int li = ks * kKs + M::kidx(lane, j);
+          const int l = l0 + li;
+          const bool on = l >= row && l < lim && row < lim;
+          const float v = cbc[ks][j] * exp_split(sls[buf][li] - s_row);
+          m[j] = on ? v : 0.f;
+        }
+        const typename M::Frag a = M::from_float(m);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+          M::mma(acc[pt], a, M::load_row(&gs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+      }
     }
   }
 
-  // epilogue: dx, direct dt gradient, dD partial
-  float dd[PT];
+  // epilogue through LDS: dx = dt'_s (T1 + T2) + D G_s, ddt'_s = x_s . (T1 + T2), dD partial
+  __syncthreads();  // every wave is done reading dy from the buffer ys reuses
 #pragma unroll
-  for (int pt = 0; pt < PT; ++pt) dd[pt] = 0.f;
+  for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int s = rowbase + 4 * (lane >> 4) + j;
+    for (int j = 0; j < 4; ++j) ys[16 * w + 4 * (lane >> 4) + j][pt * 16 + (lane & 15)] = acc[pt][j];
+  __syncthreads();
+  const char* xbase = (const char*)k.x + (b * k.sx[0] + t0 * k.sx[1] + hh * k.sx[2]) * ES;
+  const int col = (tid % RPT) * VE;  // fixed per thread: kThreads is a multiple of RPT
+  float dd[VE];
+#pragma unroll
+  for (int q = 0; q < VE; ++q) dd[q] = 0.f;
+  float Dv[VE];
+#pragma unroll
+  for (int q = 0; q < VE; ++q)
+    Dv[q] = !k.has_D ? 0.f : k.D_hdim ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : k.Dp[hh * k.sD[0]];
+  for (int e = tid; e < 64 * RPT; e += kThreads) {  // uniform trip count over the block
+    const int r = e / RPT;
+    const int s = lt * 64 + r;
     const bool valid = s < lim;
-    const int64_t t = t0 + (valid ? s : 0);
+    Raw xr[VE], gr[VE];
+    if (valid) {
+      load16<T>(xbase + (s * k.sx[1] + col) * ES, xr);
+      load16<T>(gbase + (s * k.sdy[1] + col) * ES, gr);
+    } else {
+#pragma unroll
+      for (int q = 0; q < VE; ++q) xr[q] = gr[q] = M::to_raw(0.f);
+    }
     const float dts = valid ? dq[s] : 0.f;
     float xsum = 0.f;
+    Raw o[VE];
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) {
-      const int p = pt * 16 + (lane & 15);
-      const float xv = valid ? Elem<T>::load(k.x, b * k.sx[0] + t * k.sx[1] + hh * k.sx[2] + p) : 0.f;
-      const float gv = valid ? Elem<T>::load(k.dy, b * k.sdy[0] + t * k.sdy[1] + hh * k.sdy[2] + p) : 0.f;
-      const float a = acc[pt][j];
+    for (int q = 0; q < VE; ++q) {
+      const float a = ys[r][col + q];
+      const float xv = M::from_raw(xr[q]), gvv = M::from_raw(gr[q]);
       xsum = fmaf(xv, a, xsum);
-      dd[pt] = fmaf(gv, xv, dd[pt]);
-      if (valid) {
-        float dxv = dts * a;
-        if (k.has_D) {
-          const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + p * k.sD[1]] : k.Dp[hh * k.sD[0]];
-          dxv = fmaf(Dv, gv, dxv);
-        }
-        Elem<T>::store(k.dx, b * k.sdx[0] + t * k.sdx[1] + hh * k.sdx[2] + p, dxv);
-      }
+      dd[q] = fmaf(gvv, xv, dd[q]);
+      o[q] = M::to_raw(fmaf(Dv[q], gvv, dts * a));
     }
-    xsum = wave_sum16(xsum);
-    if ((lane & 15) == 0 && valid) k.ddtd[hrow + s] = xsum;
+    if (valid)
+      *reinterpret_cast<u4*>((char*)k.dx + (b * k.sdx[0] + (t0 + s) * k.sdx[1] + hh * k.sdx[2] + col) * ES) =
+          *reinterpret_cast<const u4*>(o);
+#pragma unroll
+    for (int m = 1; m < RPT; m <<= 1) xsum += __shfl_xor(xsum, m);  // the row's RPT lanes are adjacent
+    if ((tid % RPT) == 0 && valid) k.ddtd[hrow + s] = xsum;
   }
   if (k.has_D) {
+    // sum dd over the threads holding the same columns: lanes that differ in bits >= log2(RPT)
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) {
-      float v = dd[pt];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (lane < 16) dred[w][pt * 16 + lane] = v;
+    for (int q = 0; q < VE; ++q) {
+      float v = dd[q];
+#pragma unroll
+      for (int m = RPT; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+      dd[q] = v;
     }
+    if (lane < RPT)
+#pragma unroll
+      for (int q = 0; q < VE; ++q) dred[w][col + q] = dd[q];
     __syncthreads();
     const int64_t brow = (b * k.K + c) * (k.Q / 64) + lt;
     if (k.D_hdim) {
