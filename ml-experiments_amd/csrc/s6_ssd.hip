@@ -90,11 +90,19 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   constexpr int NT = (P / 16) * NTN;
   constexpr int TPW = (NT + 3) / 4;
   constexpr int ES = sizeof(Raw);
-  constexpr int NB = 2 * (P + N) * kLp * ES <= 65536 ? 2 : 1;
+  // 16-bit types: slices stay row-major in LDS (16-byte stores, rows l) and the MFMA operands
+  // come through transposing reads; fp32: slices are written transposed (rows p / n).
+  constexpr bool TR = ES == 2;
+  constexpr int XPT = P + 16, BPT = N + 16;                      // row-major pitches (TR)
+  constexpr int SLICE_BYTES = TR ? kKs * (XPT + BPT) * ES : (P + N) * kLp * ES;
+  constexpr int NB = 2 * SLICE_BYTES <= 65536 ? 2 : 1;
   constexpr int XC = kKs * (P / VE), BC = kKs * (N / VE);       // 16-byte chunks per slice
   constexpr int XL = (XC + kThreads - 1) / kThreads, BL = (BC + kThreads - 1) / kThreads;
-  __shared__ __attribute__((aligned(16))) Raw xs[NB][P][kLp];
-  __shared__ __attribute__((aligned(16))) Raw bs[NB][N][kLp];
+  __shared__ __attribute__((aligned(16))) char smem[NB * SLICE_BYTES];
+  Raw (*xs)[P][kLp] = reinterpret_cast<Raw (*)[P][kLp]>(smem);
+  Raw (*bs)[N][kLp] = reinterpret_cast<Raw (*)[N][kLp]>(smem + NB * P * kLp * ES);
+  Raw (*xr)[kKs][XPT] = reinterpret_cast<Raw (*)[kKs][XPT]>(smem);
+  Raw (*br)[kKs][BPT] = reinterpret_cast<Raw (*)[kKs][BPT]>(smem + NB * kKs * XPT * ES);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // work id -> (head fastest, chunk, batch): the heads of one chunk share its B (C) rows
   const int64_t wid = xcd_work_id();
@@ -157,8 +165,12 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       const int e = tid + i * kThreads;
       if (e < XC) {
         const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+        if constexpr (TR) {
+          *reinterpret_cast<u4*>(&xr[buf][r][col]) = *reinterpret_cast<const u4*>(xv[i]);
+        } else {
 #pragma unroll
-        for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
+          for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
+        }
       }
     }
 #pragma unroll
@@ -166,8 +178,15 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       const int e = tid + i * kThreads;
       if (e < BC) {
         const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+        Raw o[VE];
 #pragma unroll
-        for (int q = 0; q < VE; ++q) bs[buf][col + q][r] = M::to_raw(M::from_raw(bv[i][q]) * wv[i]);
+        for (int q = 0; q < VE; ++q) o[q] = M::to_raw(M::from_raw(bv[i][q]) * wv[i]);
+        if constexpr (TR) {
+          *reinterpret_cast<u4*>(&br[buf][r][col]) = *reinterpret_cast<const u4*>(o);
+        } else {
+#pragma unroll
+          for (int q = 0; q < VE; ++q) bs[buf][col + q][r] = o[q];
+        }
       }
     }
     __syncthreads();
@@ -177,8 +196,14 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       const int ti = w + 4 * i;
       if (ti < NT) {
         const int pt = ti / NTN, nt = ti % NTN;
-        const typename M::Frag a = M::load_row(&xs[buf][pt * 16 + (lane & 15)][0], lane);
-        const typename M::Frag bf = M::load_row(&bs[buf][nt * 16 + (lane & 15)][0], lane);
+        typename M::Frag a, bf;
+        if constexpr (TR) {
+          a = M::load_tr(&xr[buf][0][pt * 16], XPT, lane);
+          bf = M::load_tr(&br[buf][0][nt * 16], BPT, lane);
+        } else {
+          a = M::load_row(&xs[buf][pt * 16 + (lane & 15)][0], lane);
+          bf = M::load_row(&bs[buf][nt * 16 + (lane & 15)][0], lane);
+        }
         M::mma(acc[i], a, bf);
       }
     }

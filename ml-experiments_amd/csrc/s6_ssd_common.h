@@ -28,6 +28,24 @@ template <> struct Mma<bf16> {
   __device__ static inline Frag load_row(const Raw* row_k0, int lane) {
     return *reinterpret_cast<const Frag*>(row_k0 + 8 * (lane >> 4));
   }
+  // Operand fragment of the 16 columns starting at tile[0][0] over K = 32 rows of a
+  // row-major LDS tile (K along rows, pitch in elements, rows 8-byte aligned), through
+  // gfx950's transposing LDS read.  ds_read_b64_tr_b16 returns to lane i of each 16-lane
+  // group element i % 4 of the 8-byte chunks addressed by lanes 4 j + i / 4 (j < 4), as
+  // measured on the device; so lane 16 g + s addresses row 8 g + 4 h + s / 4, column
+  // 4 (s % 4), and the reads h = 0, 1 return this lane's k = 8 g + 4 h .. + 3.
+  __device__ static inline Frag load_tr(const Raw* tile, int pitch, int lane) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const int g = lane >> 4, s = lane & 15;
+    const Raw* p0 = tile + (8 * g + (s >> 2)) * pitch + 4 * (s & 3);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(p0));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(p0 + 4 * pitch));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(Frag, both);
+  }
   __device__ static inline Frag from_float(const float (&v)[8]) {
     Frag f;
 #pragma unroll
