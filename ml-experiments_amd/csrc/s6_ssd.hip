@@ -317,12 +317,16 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   constexpr int YP = P + 4;                                // y staging pitch (floats)
   constexpr int HCH = N < 128 ? N : ((ES == 4 && P == 128) ? 64 : 128);  // H columns per stage
   constexpr int HP = HCH + 8;                              // H staging pitch, 16-byte rows
-  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
+  constexpr bool TR = ES == 2;                             // row-major x + transposing reads
+  constexpr int XPT = P + 16;                              // row-major x pitch (TR)
+  constexpr int XS_BYTES = TR ? 2 * KST * XPT * ES : 2 * P * LP * ES;
+  constexpr int YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
   constexpr int SM_A = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
   constexpr int SM_BYTES = SM_A > HS_BYTES ? SM_A : HS_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[SM_BYTES];
   __shared__ float sls[2][KST], dls[2][KST];
   Raw (*xs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
+  Raw (*xr)[KST][XPT] = reinterpret_cast<Raw (*)[KST][XPT]>(smem);
   float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
   Raw (*hsm)[HP] = reinterpret_cast<Raw (*)[HP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -435,8 +439,12 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
       const int e = tid + i * kThreads;
       if (e < XC) {
         const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+        if constexpr (TR) {
+          *reinterpret_cast<u4*>(&xr[buf][r][col]) = *reinterpret_cast<const u4*>(xv[i]);
+        } else {
 #pragma unroll
-        for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
+          for (int q = 0; q < VE; ++q) xs[buf][col + q][r] = xv[i][q];
+        }
       }
     }
     if (tid < KST) {
@@ -464,8 +472,10 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
         }
         const typename M::Frag a = M::from_float(m);
 #pragma unroll
-        for (int pt = 0; pt < PT; ++pt)
-          M::mma(acc[pt], a, M::load_row(&xs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+        for (int pt = 0; pt < PT; ++pt) {
+          if constexpr (TR) M::mma(acc[pt], a, M::load_tr(&xr[buf][ks * kKs][pt * 16], XPT, lane));
+          else M::mma(acc[pt], a, M::load_row(&xs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+        }
       }
     }
   }

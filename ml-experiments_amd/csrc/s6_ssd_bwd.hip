@@ -136,7 +136,10 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   constexpr int YP = P + 4;                                // T staging pitch (floats)
   constexpr int HCH = N < 128 ? N : ((ES == 4 && P == 128) ? 64 : 128);  // dst columns per stage
   constexpr int HP = HCH + 8;
-  constexpr int XS_BYTES = 2 * P * LP * ES, YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
+  constexpr bool TR = ES == 2;                             // row-major dy + transposing reads
+  constexpr int GPT = P + 16;                              // row-major dy pitch (TR)
+  constexpr int XS_BYTES = TR ? 2 * KST * GPT * ES : 2 * P * LP * ES;
+  constexpr int YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
   constexpr int SM_A = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
   constexpr int SM_BYTES = SM_A > HS_BYTES ? SM_A : HS_BYTES;
   constexpr int RPT = P / VE;                              // threads per row in the epilogue
@@ -144,6 +147,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   __shared__ float sls[2][KST];
   __shared__ float dred[kThreads / kWave][P];
   Raw (*gs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
+  Raw (*gr_)[KST][GPT] = reinterpret_cast<Raw (*)[KST][GPT]>(smem);
   float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
   Raw (*dsm)[HP] = reinterpret_cast<Raw (*)[HP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -253,8 +257,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
       const int e = tid + i * kThreads;
       if (e < XC) {
         const int r = e / (P / VE), col = (e % (P / VE)) * VE;
+        if constexpr (TR) {
+          *reinterpret_cast<u4*>(&gr_[buf][r][col]) = *reinterpret_cast<const u4*>(gv[i]);
+        } else {
 #pragma unroll
-        for (int q = 0; q < VE; ++q) gs[buf][col + q][r] = gv[i][q];
+          for (int q = 0; q < VE; ++q) gs[buf][col + q][r] = gv[i][q];
+        }
       }
     }
     if (tid < KST) sls[buf][tid] = sv;
@@ -279,8 +287,10 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
         }
         const typename M::Frag a = M::from_float(m);
 #pragma unroll
-        for (int pt = 0; pt < PT; ++pt)
-          M::mma(acc[pt], a, M::load_row(&gs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+        for (int pt = 0; pt < PT; ++pt) {
+          if constexpr (TR) M::mma(acc[pt], a, M::load_tr(&gr_[buf][ks * kKs][pt * 16], GPT, lane));
+          else M::mma(acc[pt], a, M::load_row(&gs[buf][pt * 16 + (lane & 15)][ks * kKs], lane));
+        }
       }
     }
   }
@@ -377,12 +387,17 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
   constexpr int NC = N < 64 ? N : 64;       // dstate columns per block
   constexpr int NS = N / NC;
   constexpr int NT = NC / 16;
-  constexpr int MP = P + 8;                 // LDS pitch, 16-byte rows
-  constexpr int NB = 2 * NC * MP * ES <= 40960 ? 2 : 1;
+  constexpr int MP = P + 8;                 // LDS pitch, 16-byte rows (transposed, fp32)
+  constexpr bool TR = ES == 2;              // 16-bit: row-major slice + transposing reads
+  constexpr int RPT_ = NC + 16;             // row-major pitch (TR)
+  constexpr int BUF_BYTES = TR ? P * RPT_ * ES : NC * MP * ES;
+  constexpr int NB = 2 * BUF_BYTES <= 40960 ? 2 : 1;
   constexpr int MC = P * (NC / VE);         // 16-byte chunks of one head's matrix slice
   constexpr int ML = (MC + kThreads - 1) / kThreads;
   constexpr int KF = P / kKs;
-  __shared__ __attribute__((aligned(16))) Raw ms[NB][NC][MP];
+  __shared__ __attribute__((aligned(16))) char smem[NB * BUF_BYTES];
+  Raw (*ms)[NC][MP] = reinterpret_cast<Raw (*)[NC][MP]>(smem);
+  Raw (*mr)[P][RPT_] = reinterpret_cast<Raw (*)[P][RPT_]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int QT = (int)(k.Q / 64);
   const int64_t wid = xcd_work_id();  // (column slice fastest, row tile, chunk, batch * group)
@@ -426,7 +441,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
 #pragma unroll
     for (int i = 0; i < ML; ++i) {
       const int e = tid + i * kThreads;
-      const int p = e % P, n0 = (e / P) * VE;
+      const int p = TR ? e / (NC / VE) : e % P, n0 = TR ? (e % (NC / VE)) * VE : (e / P) * VE;
       if (e < MC) load16<T>(mat + p * N + ns * NC + n0, mv[i]);
     }
 #pragma unroll
@@ -451,9 +466,14 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
     for (int i = 0; i < ML; ++i) {
       const int e = tid + i * kThreads;
       if (e < MC) {
-        const int p = e % P, n0 = (e / P) * VE;
+        if constexpr (TR) {
+          const int p = e / (NC / VE), n0 = (e % (NC / VE)) * VE;
+          *reinterpret_cast<u4*>(&mr[buf][p][n0]) = *reinterpret_cast<const u4*>(mv[i]);
+        } else {
+          const int p = e % P, n0 = (e / P) * VE;
 #pragma unroll
-        for (int q = 0; q < VE; ++q) ms[buf][n0 + q][p] = mv[i][q];
+          for (int q = 0; q < VE; ++q) ms[buf][n0 + q][p] = mv[i][q];
+        }
       }
     }
     Frag ac[KF];
@@ -471,8 +491,10 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
 #pragma unroll
     for (int kk = 0; kk < KF; ++kk)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        M::mma(acc[nt], ac[kk], M::load_row(&ms[buf][nt * 16 + (lane & 15)][kk * kKs], lane));
+      for (int nt = 0; nt < NT; ++nt) {
+        if constexpr (TR) M::mma(acc[nt], ac[kk], M::load_tr(&mr[buf][kk * kKs][nt * 16], RPT_, lane));
+        else M::mma(acc[nt], ac[kk], M::load_row(&ms[buf][nt * 16 + (lane & 15)][kk * kKs], lane));
+      }
     const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -669,7 +691,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
   constexpr int VE = M::kVe;
   constexpr int NT = N / 16;
   constexpr int ES = sizeof(Raw);
-  __shared__ __attribute__((aligned(16))) Raw os[N][kLp];
+  constexpr bool TR = ES == 2;  // 16-bit: row-major slice + transposing reads
+  constexpr int OPT = N + 16;
+  constexpr int OS_BYTES = TR ? kKs * OPT * ES : N * kLp * ES;
+  __shared__ __attribute__((aligned(16))) char smem[OS_BYTES];
+  Raw (*os)[kLp] = reinterpret_cast<Raw (*)[kLp]>(smem);
+  Raw (*orr)[OPT] = reinterpret_cast<Raw (*)[OPT]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t wid = xcd_work_id();  // (row tile fastest, chunk, batch * group)
   const int lt = (int)(wid % (k.Q / 64));
@@ -696,8 +723,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
       else
 #pragma unroll
         for (int q = 0; q < VE; ++q) v[q] = M::to_raw(0.f);
+      if constexpr (TR) {
+        *reinterpret_cast<u4*>(&orr[r][col]) = *reinterpret_cast<const u4*>(v);
+      } else {
 #pragma unroll
-      for (int q = 0; q < VE; ++q) os[col + q][r] = v[q];
+        for (int q = 0; q < VE; ++q) os[col + q][r] = v[q];
+      }
     }
     __syncthreads();
     const bool reach = MODE == 0 ? s0 <= rowbase + 15 : s0 + kKs - 1 >= rowbase;  // wave-uniform
@@ -712,7 +743,10 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
       }
       const typename M::Frag a = M::from_float(m);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) M::mma(acc[nt], a, M::load_row(&os[nt * 16 + (lane & 15)][0], lane));
+      for (int nt = 0; nt < NT; ++nt) {
+        if constexpr (TR) M::mma(acc[nt], a, M::load_tr(&orr[0][nt * 16], OPT, lane));
+        else M::mma(acc[nt], a, M::load_row(&os[nt * 16 + (lane & 15)][0], lane));
+      }
     }
   }
   const float* part = MODE == 0 ? k.dCp : k.dBp;
