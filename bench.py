@@ -368,12 +368,23 @@ def ssd_flops(c):
     return 4 * B * L * H * P * N + B * L * H * P * Q + B * L * G * Q * N
 
 
+def ssd_scan_bytes(c):
+    """Algorithmic HBM bytes of one ssd_chunk_scan launch, each tensor once: x read and out
+    written (bf16), C (bf16), the passed states (bf16, one per chunk and head), the
+    lower-triangle 64x64 tiles of C B^T (fp32) and the processed dt and cumsums (fp32)."""
+    B, L, H, P, G, N, Q = (c["batch"], c["seqlen"], c["nheads"], c["headdim"], c["ngroups"],
+                           c["dstate"], c["chunk"])
+    K, qt = -(-L // Q), Q // 64
+    return (2 * B * L * H * P * 2 + B * L * G * N * 2 + B * K * H * P * N * 2
+            + B * K * G * (qt * (qt + 1) // 2) * 64 * 64 * 4 + 2 * B * H * K * Q * 4)
+
+
 def run_ssd(torch, args):
     """Workload ssd2: Mamba-2's default SSD layer (headdim 64, dstate 128, chunk 256, one
     group, D per head, dt bias + softplus, no z: the RMSNorm variant, mamba2.py:30-56,
     209-225) at 24 heads (d_model 768), batch 8, seqlen 8192, bf16: one forward and one
     forward + backward of mamba_chunk_scan_combined."""
-    from s6scan.ssd_combined import mamba_chunk_scan_combined
+    from s6scan.ssd_combined import mamba_chunk_scan_combined, ssd_forward
     c = SSD2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -391,11 +402,11 @@ def run_ssd(torch, args):
     D = torch.randn(H, generator=g).to(dev).requires_grad_(True)
     bias = (0.3 * torch.randn(H, generator=g)).to(dev).requires_grad_(True)
 
-    def fwd(i):
+    def fwd(i, ev=None):  # the forward launch sequence mamba_chunk_scan_combined runs
         s_ = sets[i % 2]
         with torch.no_grad():
-            mamba_chunk_scan_combined(s_["x"], s_["dt"], A, s_["B"], s_["C"], Q, D=D,
-                                      dt_bias=bias, dt_softplus=True)
+            ssd_forward(s_["x"], s_["dt"], A, s_["B"], s_["C"], Q, D=D, dt_bias=bias,
+                        dt_softplus=True, kernel_events=ev)
 
     def fwdbwd(i):
         s_ = sets[i % 2]
@@ -405,15 +416,27 @@ def run_ssd(torch, args):
         out.backward(s_["dy"])
 
     res_t = {}
+    mk = lambda: torch.cuda.Event(enable_timing=True)
+    evs = [(mk(), mk()) for _ in range(args.steps)]
+    for e0, e1 in evs:  # create the events; the library re-records them around ssd_chunk_scan
+        e0.record(), e1.record()
     for name, fn in (("fwd", fwd), ("fwdbwd", fwdbwd)):
         for i in range(args.warmup):
             fn(i)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(args.steps):
-            fn(i)
+            fn(i, evs[i]) if name == "fwd" else fn(i)
         torch.cuda.synchronize()
         res_t[name] = (time.perf_counter() - t0) * 1e3 / args.steps
+    scan_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / len(evs)
+    scan_gbps = ssd_scan_bytes(c) / (scan_ms * 1e-3) / 1e9
+    traffic = None  # HBM bytes per ssd_chunk_scan launch, from the committed rocprofv3 counters
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            prof = json.load(f).get("ssd2")
+        if prof:
+            traffic = round(prof["traffic_bytes_per_launch"])
     tokch = B * L * H * P
     fl = ssd_flops(c)
     res = {
@@ -429,6 +452,10 @@ def run_ssd(torch, args):
         "fwd_mtok_ch_per_s": round(tokch / (res_t["fwd"] * 1e-3) / 1e6, 2),
         "fwd_achieved": {"hbm_GBps_io_only": round(ssd_bytes(c, False) / (res_t["fwd"] * 1e-3) / 1e9, 2),
                          "mfma_TFLOPs": round(fl / (res_t["fwd"] * 1e-3) / 1e12, 2)},
+        "roofline": {"kernel": "ssd_chunk_scan", "bound": "hbm", "achieved": round(scan_gbps, 2),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(scan_gbps / 8000.0, 5),
+                     "traffic": traffic, "kernel_ms": round(scan_ms, 5),
+                     "algorithmic_bytes": ssd_scan_bytes(c)},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline ...")

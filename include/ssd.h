@@ -62,6 +62,10 @@ typedef struct S6SsdFwdArgs {
   void* out_x;                 int64_t out_x_stride[4];   /* y before the z gate; NULL = not written */
   float* final_states;         /* NULL = not written */
   void* workspace;             size_t workspace_bytes;
+  /* Optional hipEvent_t pair (NULL = off), recorded on the call's stream right before and
+   * after the chunk-scan kernel, so a caller can time that kernel alone.  No counterpart in
+   * the reference; it exists for roofline measurement. */
+  void* kernel_events[2];
 } S6SsdFwdArgs;
 
 typedef struct S6SsdBwdArgs {

@@ -479,7 +479,7 @@ int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream) {
   const S6SsdProblem& p = a->p;
   const SsdPlan pl = ssd_plan(p);
   s6::SsdK k = ssd_fill(*a, pl);
-  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream);
+  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream, a->kernel_events);
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_fwd: %s", hipGetErrorString(e));
   return ok();
 }

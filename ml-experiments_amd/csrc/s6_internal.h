@@ -223,7 +223,7 @@ hipError_t launch_conv_bwd(const ConvK& k, int io_dtype, int width, int vec, boo
 // s6_ssd.hip: the Mamba-2 SSD forward; prep = dt processing, chunk states, state passing
 // and C B^T (shared with the backward, which recomputes them); dstates = the chunk-state
 // kernel in its backward mode (gradient of each chunk's entering state).
-hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st);
+hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st, void* const* ev = nullptr);
 hipError_t launch_ssd_prep(const SsdK& k, hipStream_t st);
 hipError_t launch_ssd_dstates(const SsdK& k, hipStream_t st);
 // s6_ssd_bwd.hip: the Mamba-2 SSD backward.

@@ -600,9 +600,11 @@ hipError_t launch_ssd_prep(const SsdK& k, hipStream_t st) { return ssd_prep(k, s
 
 hipError_t launch_ssd_dstates(const SsdK& k, hipStream_t st) { return ssd_dstates(k, st); }
 
-hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st) {
+hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st, void* const* ev) {
   hipError_t e = ssd_prep(k, st);
-  return e != hipSuccess ? e : ssd_scan(k, st);
+  if (e != hipSuccess || (e = record_event(ev, 0, st)) != hipSuccess) return e;
+  if ((e = ssd_scan(k, st)) != hipSuccess) return e;
+  return record_event(ev, 1, st);
 }
 
 }  // namespace s6

@@ -15,7 +15,7 @@ import os
 
 import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 64
@@ -165,6 +165,7 @@ class S6SsdFwdArgs(ctypes.Structure):
         ("out_x", _vp), ("out_x_stride", _a(4)),
         ("final_states", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("kernel_events", _vp * 2),
     ]
 
 

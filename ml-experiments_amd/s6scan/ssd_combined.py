@@ -111,9 +111,11 @@ def _fill_inputs(a, x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx):
 
 def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initial_states=None,
                 seq_idx=None, dt_softplus=False, dt_limit=(0.0, float("inf")),
-                want_final_states=False, want_out_x=False):
+                want_final_states=False, want_out_x=False, kernel_events=None):
     """One forward launch sequence.  Returns (out, out_x, final_states); out_x (the output
-    before the z gate) only with z and ``want_out_x``, final_states only when asked."""
+    before the z gate) only with z and ``want_out_x``, final_states only when asked.
+    ``kernel_events``: optional pair of torch.cuda.Events that the library records right
+    before and after its chunk-scan kernel (measurement only)."""
     batch, seqlen, nheads, headdim = x.shape
     dstate = B.shape[-1]
     x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx = _prepare(
@@ -134,6 +136,8 @@ def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initia
         nbytes = _lib.LIB.s6_ssd_fwd_workspace_bytes(ctypes.byref(a.p))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         a.workspace, a.workspace_bytes = _ptr(ws), nbytes
+        if kernel_events is not None:
+            a.kernel_events[0], a.kernel_events[1] = (e.cuda_event for e in kernel_events)
         stream = torch.cuda.current_stream(x.device).cuda_stream
         _lib.check(_lib.LIB.s6_ssd_fwd(ctypes.byref(a), ctypes.c_void_p(stream)), "s6_ssd_fwd")
     return out, out_x, final
