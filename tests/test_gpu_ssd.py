@@ -60,6 +60,9 @@ CASES = [  # batch, L, H, P, G, N, chunk, opts
     (1, 1000, 2, 64, 1, 256, 256, ("z", "init")),
     (2, 190, 8, 64, 1, 128, 64, ("seq", "init", "z", "D", "bias")),
     (1, 64, 1, 32, 1, 32, 64, ()),
+    # workgroup counts that are not multiples of the 8 XCDs (54 chunk-scan blocks, 27
+    # dCB tiles, 18 row blocks): the uneven branch of the XCD work mapping
+    (3, 330, 3, 64, 1, 64, 128, ("D", "bias", "z")),
 ]
 
 
@@ -114,6 +117,7 @@ GRAD_CASES = [  # batch, L, H, P, G, N, chunk, opts
     (2, 256, 3, 128, 3, 32, 256, ("limit", "bias")),
     (1, 200, 2, 64, 1, 256, 64, ("z", "init", "bias", "final")),
     (2, 130, 4, 32, 2, 32, 64, ("seq", "z", "D")),
+    (3, 330, 3, 64, 1, 64, 128, ("D", "bias", "init", "final")),
 ]
 
 
