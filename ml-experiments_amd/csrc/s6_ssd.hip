@@ -223,29 +223,62 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
 
 // ---- 3. state passing across chunks --------------------------------------------------
 
+// Sequential over chunks, 4 state elements per thread; each chunk's inputs (the chunk
+// state and its decay) are loaded two chunks ahead, so the chain's loads overlap.
+constexpr int kSpEpt = 4;  // elements per thread (P N is a multiple of 1024)
+
 template <typename T>
 __global__ void __launch_bounds__(kThreads) ssd_state_pass(SsdK k) {
   typedef typename Mma<T>::Raw Raw;
   const int64_t PN = k.P * k.N;
-  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (e >= PN) return;
   const int64_t hh = blockIdx.y, b = blockIdx.z;
-  const int64_t p = e / k.N, n = e % k.N;
-  float H = k.has_init ? k.init[b * k.sinit[0] + hh * k.sinit[1] + p * k.sinit[2] + n * k.sinit[3]] : 0.f;
-  int32_t seq_prev = 0;
+  int64_t e[kSpEpt];
+  float H[kSpEpt];
+#pragma unroll
+  for (int i = 0; i < kSpEpt; ++i) {
+    e[i] = (int64_t)blockIdx.x * (kThreads * kSpEpt) + threadIdx.x + i * kThreads;
+    const int64_t p = e[i] / k.N, n = e[i] % k.N;
+    H[i] = k.has_init ? k.init[b * k.sinit[0] + hh * k.sinit[1] + p * k.sinit[2] + n * k.sinit[3]] : 0.f;
+  }
   Raw* hs = (Raw*)k.hs;
-  for (int64_t c = 0; c < k.K; ++c) {
-    const int64_t o = ((b * k.K + c) * k.H + hh) * PN + e;
-    hs[o] = Mma<T>::to_raw(H);
-    float scale = exp_split(k.dacs[((b * k.H + hh) * k.K + c) * k.Q + k.Q - 1]);
+  const float* sl = k.dacs + (b * k.H + hh) * k.K * k.Q + k.Q - 1;  // S_last of chunk c: sl[c * Q]
+  auto ofs = [&](int64_t c) { return ((b * k.K + c) * k.H + hh) * PN; };
+  float sa[kSpEpt], sb[kSpEpt], la = 0.f, lb = 0.f;
+  auto fetch = [&](int64_t c, float (&v)[kSpEpt], float& l) {
+    if (c >= k.K) return;
+#pragma unroll
+    for (int i = 0; i < kSpEpt; ++i) v[i] = k.st[ofs(c) + e[i]];
+    l = sl[c * k.Q];
+  };
+  fetch(0, sa, la);
+  fetch(1, sb, lb);
+  int32_t seq_prev = 0;
+  auto step = [&](int64_t c, float (&v)[kSpEpt], float& l) {
+    float scale = exp_split(l);
     if (k.has_seq) {
       const int32_t sn = seq_at(k, b, min((c + 1) * k.Q, k.L) - 1);
       if (sn != seq_prev) scale = 0.f;
       seq_prev = sn;
     }
-    H = scale * H + k.st[o];
+    const int64_t o = ofs(c);
+    float cur[kSpEpt];
+#pragma unroll
+    for (int i = 0; i < kSpEpt; ++i) cur[i] = v[i];
+    fetch(c + 2, v, l);
+#pragma unroll
+    for (int i = 0; i < kSpEpt; ++i) {
+      hs[o + e[i]] = Mma<T>::to_raw(H[i]);
+      H[i] = fmaf(scale, H[i], cur[i]);
+    }
+  };
+  for (int64_t c = 0; c < k.K; c += 2) {
+    step(c, sa, la);
+    if (c + 1 < k.K) step(c + 1, sb, lb);
   }
-  if (k.final_states) k.final_states[(b * k.H + hh) * PN + e] = H;
+  if (k.final_states) {
+#pragma unroll
+    for (int i = 0; i < kSpEpt; ++i) k.final_states[(b * k.H + hh) * PN + e[i]] = H[i];
+  }
 }
 
 // ---- 4. C B^T within each chunk ------------------------------------------------------
@@ -539,7 +572,7 @@ hipError_t ssd_prep_pn(const SsdK& k, hipStream_t st) {
   hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 0>), dim3((unsigned)(k.K * k.H * k.Bsz)),
                      dim3(kThreads), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_state_pass<T>), dim3((unsigned)((P * N + kThreads - 1) / kThreads),
+  hipLaunchKernelGGL((ssd_state_pass<T>), dim3((unsigned)(P * N / (kThreads * kSpEpt)),
                      (unsigned)k.H, (unsigned)k.Bsz), dim3(kThreads), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const int qt = (int)(k.Q / 64);

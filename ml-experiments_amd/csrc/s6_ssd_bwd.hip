@@ -81,19 +81,35 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_bwd(SsdK k) {
   }
   const Raw* hs = (const Raw*)k.hs;
   Raw* dst = (Raw*)k.dst;
+  // the next (earlier) chunk's H and dHl are loaded while this one is processed
+  auto ofs = [&](int64_t c) { return ((b * k.K + c) * k.H + hh) * PN; };
+  float hn[kSpbPer], gn[kSpbPer];
+  auto fetch = [&](int64_t c) {
+    if (c < 0) return;
+#pragma unroll
+    for (int i = 0; i < kSpbPer; ++i) {
+      hn[i] = Mma<T>::from_raw(hs[ofs(c) + e[i]]);
+      gn[i] = k.dhl[ofs(c) + e[i]];
+    }
+  };
+  fetch(k.K - 1);
   for (int64_t c = k.K - 1; c >= 0; --c) {
     float scale = exp_split(k.dacs[((b * k.H + hh) * k.K + c) * k.Q + k.Q - 1]);
     if (k.has_seq) {
       const int32_t prev = c > 0 ? seq_last_of(k, b, c - 1) : 0;
       if (seq_last_of(k, b, c) != prev) scale = 0.f;
     }
-    const int64_t o = ((b * k.K + c) * k.H + hh) * PN;
+    const int64_t o = ofs(c);
+    float hc[kSpbPer], gc[kSpbPer];
+#pragma unroll
+    for (int i = 0; i < kSpbPer; ++i) { hc[i] = hn[i]; gc[i] = gn[i]; }
+    fetch(c - 1);
     float part = 0.f;
 #pragma unroll
     for (int i = 0; i < kSpbPer; ++i) {
       dst[o + e[i]] = Mma<T>::to_raw(dH[i]);
-      part = fmaf(dH[i], Mma<T>::from_raw(hs[o + e[i]]), part);
-      dH[i] = fmaf(scale, dH[i], k.dhl[o + e[i]]);
+      part = fmaf(dH[i], hc[i], part);
+      dH[i] = fmaf(scale, dH[i], gc[i]);
     }
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) part += __shfl_xor(part, m);
