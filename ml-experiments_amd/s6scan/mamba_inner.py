@@ -49,6 +49,33 @@ def _as_bcl(flat, batch, seqlen):
     return flat.view(batch, seqlen, flat.shape[-1]).mT
 
 
+def _wgrad(a, b):
+    """``a.t() @ b`` for token-major ``a`` [T, M] and ``b`` [T, N]: the weight gradients of
+    the block's projections, T = batch * seqlen.  As one GEMM the output is small and T long,
+    so the product runs on few workgroups.  T is split into S slices, one batched product with
+    fp32 partials, summed in a fixed order and rounded once to the product's dtype (autocast's
+    when it is on, as the reference's ``@`` under autocast) -- the rounding point of the
+    single product."""
+    dev = a.device.type
+    dt = (torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev)
+          else torch.promote_types(a.dtype, b.dtype))
+    T, M = a.shape
+    N = b.shape[1]
+    tiles = -(-M // 64) * -(-N // 64)
+    S = 1
+    while S < 32 and S * tiles < 2048 and T % (2 * S) == 0 and T // (2 * S) >= 1024:
+        S *= 2
+    with torch.autocast(dev, enabled=False):
+        a, b = a.to(dt), b.to(dt).contiguous()
+        if S == 1:
+            return a.t() @ b
+        a3 = a.reshape(S, T // S, M).transpose(1, 2)
+        b3 = b.view(S, T // S, N)  # the right operand stays contiguous
+        part = (torch.bmm(a3, b3, out_dtype=torch.float32) if dt != torch.float32
+                else torch.bmm(a3, b3))
+        return part.sum(0).to(dt)
+
+
 def _flat(bcl):
     """[batch, C, seqlen] channel-last view -> [(batch seqlen), C] view."""
     batch, c, seqlen = bcl.shape
@@ -132,7 +159,7 @@ class MambaInnerFn(torch.autograd.Function):
         (dconv1d_out, ddelta, dA, dB, dC, dD, _, ddelta_bias, out_z) = selective_scan_backward(
             conv1d_out, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout_y, x_ckpt,
             out=out, dz_out=dz, recompute_out_z=True, kernel_events=KERNEL_EVENTS)
-        dout_proj_weight = dout.t() @ _flat(out_z)
+        dout_proj_weight = _wgrad(dout, _flat(out_z))
         dout_proj_bias = dout.sum(dim=0) if not ctx.out_proj_bias_is_None else None
         dD = dD if D is not None else None
         dx_dbl = torch.empty_like(x_dbl)
@@ -149,10 +176,10 @@ class MambaInnerFn(torch.autograd.Function):
             dx_dbl[:, -d_state:] = dC
             dC = None
         ddelta = _flat(ddelta)  # (bl, d_inner)
-        ddelta_proj_weight = ddelta.t() @ x_dbl[:, :delta_rank]
+        ddelta_proj_weight = _wgrad(ddelta, x_dbl[:, :delta_rank])
         dx_dbl[:, :delta_rank] = ddelta @ delta_proj_weight
         dconv = _flat(dconv1d_out)  # (bl, d_inner) view of dconv1d_out
-        dx_proj_weight = dx_dbl.t() @ _flat(conv1d_out)
+        dx_proj_weight = _wgrad(dx_dbl, _flat(conv1d_out))
         torch.addmm(dconv, dx_dbl, x_proj_weight, out=dconv)
         _, dconv1d_weight, dconv1d_bias, _ = causal_conv1d_bwd(
             x, conv1d_weight, conv1d_bias, dconv1d_out, dx=dx, silu_activation=True)

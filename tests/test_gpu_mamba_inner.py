@@ -249,3 +249,41 @@ def test_mamba_forward_matches_reference_fast_path():
     ref.sum().backward()
     for (n, pg), (_, pc) in zip(mg.named_parameters(), m.named_parameters()):
         assert_grad_close(pg.grad, pc.grad, torch.float32, n)
+
+
+@pytest.mark.parametrize("shape", [(65536, 56, 768), (65536, 768, 24), (65536, 384, 768), (6144, 40, 96)])
+def test_split_weight_gradient_matches_float64(shape):
+    """The block's weight gradients a.t() @ b over T = batch * seqlen tokens run split over T
+    (fp32 partials summed in a fixed order, one rounding); compare with float64, in fp32 and
+    under bf16 autocast (where the single product's own rounding to bf16 is the bound)."""
+    from s6scan.mamba_inner import _wgrad
+    T, M, N = shape
+    g = torch.Generator().manual_seed(M + N)
+    a, b = torch.randn(T, M, generator=g), torch.randn(T, N, generator=g)
+    ref = a.double().t() @ b.double()
+    scale = ref.abs().max().item()
+    got = _wgrad(a.to(DEV), b.to(DEV))
+    assert got.dtype == torch.float32 and got.shape == (M, N)
+    assert (got.double().cpu() - ref).abs().max().item() <= 1e-5 * scale
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ab, bb = a.to(DEV, torch.bfloat16), b.to(DEV, torch.bfloat16)
+        got16 = _wgrad(ab, bb)
+        one = ab.t() @ bb  # the single product the split replaces
+    assert got16.dtype == torch.bfloat16
+    ref16 = ab.double().cpu().t() @ bb.double().cpu()
+    err = (got16.double().cpu() - ref16).abs()
+    assert err.max().item() <= 2 ** -8 * ref16.abs().max().item()  # one bf16 rounding
+    assert err.norm().item() <= 1.05 * (one.double().cpu() - ref16).norm().item() + 1e-6
+
+
+def test_mamba_inner_fn_long_sequence_split_weight_grads():
+    """T = 2 * 2048 tokens: the weight gradients take the split path (S = 2)."""
+    p = block_params(21, batch=2, L=2048, d_model=32, d_inner=64, dt_rank=2, proj_bias=False)
+    out, lg = run_block(p, DEV, mamba_inner_fn, "cl")
+    ref, lc = run_block(p, "cpu", mamba_inner_ref)
+    assert_out_close(out, ref, torch.float32, "out", dstate=16)
+    dy = torch.randn(out.shape, generator=torch.Generator().manual_seed(22))
+    out.backward(dy.to(DEV))
+    ref.backward(dy)
+    for k in ("x_proj_weight", "delta_proj_weight", "out_proj_weight", "xz", "A", "D"):
+        assert_grad_close(lg[k].grad, lc[k].grad, torch.float32, "d" + k)
