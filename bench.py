@@ -199,7 +199,9 @@ def run_mamba(torch, args):
     def step(i):
         h, dy = sets[i % len(sets)]
         with torch.autocast("cuda", dtype=torch.bfloat16):
-            xz = torch.nn.functional.linear(h, p["in_proj_weight"]).mT
+            # in_proj as mamba_inner.mamba_forward issues it (weight gradient split over tokens)
+            xz = mamba_inner.InProjFn.apply(h.reshape(B * L, dm), p["in_proj_weight"],
+                                            None).view(B, L, -1).mT
             out = mamba_inner.mamba_inner_fn(
                 xz, p["conv1d_weight"], p["conv1d_bias"], p["x_proj_weight"],
                 p["delta_proj_weight"], p["out_proj_weight"], None, -torch.exp(p["A_log"]),

@@ -199,11 +199,37 @@ def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
                               B_proj_bias, C_proj_bias, delta_softplus)
 
 
+class InProjFn(torch.autograd.Function):
+    """``F.linear(hidden, weight, bias)`` over the tokens of a block's in_proj, with the same
+    forward and gradients as autograd's, except that the weight gradient is computed split
+    over tokens (``_wgrad``): one GEMM over batch * seqlen tokens into a small weight runs on
+    few workgroups.  Under autocast the products run in the autocast dtype and the weight
+    and bias gradients come back in the parameters' dtypes, as autograd's cast would."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, h2d, weight, bias):
+        ctx.save_for_backward(h2d, weight)
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return F.linear(h2d, weight, bias)
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dy):
+        h2d, weight = ctx.saved_tensors
+        dh = (dy @ weight).to(h2d.dtype) if ctx.needs_input_grad[0] else None
+        dw = _wgrad(dy, h2d).to(weight.dtype)
+        db = dy.sum(0).to(ctx.bias_dtype) if ctx.bias_dtype is not None else None
+        return dh, dw, db
+
+
 def mamba_forward(m, hidden_states):
     """Fast-path forward of a zoology-``Mamba``-shaped module ``m`` (mamba.py:120-153):
     in_proj, then ``mamba_inner_fn`` with input-dependent B / C, ``D``, the dt_proj bias as
     delta bias and softplus.  hidden_states: (batch, seqlen, d_model)."""
-    xz = F.linear(hidden_states, m.in_proj.weight, m.in_proj.bias).mT  # channel-last
+    batch, seqlen, d_model = hidden_states.shape
+    xz = InProjFn.apply(hidden_states.reshape(batch * seqlen, d_model), m.in_proj.weight,
+                        m.in_proj.bias).view(batch, seqlen, -1).mT  # channel-last
     A = -torch.exp(m.A_log.float())
     return mamba_inner_fn(xz, m.conv1d.weight, m.conv1d.bias, m.x_proj.weight,
                           m.dt_proj.weight, m.out_proj.weight, m.out_proj.bias, A, None, None,

@@ -287,3 +287,28 @@ def test_mamba_inner_fn_long_sequence_split_weight_grads():
     ref.backward(dy)
     for k in ("x_proj_weight", "delta_proj_weight", "out_proj_weight", "xz", "A", "D"):
         assert_grad_close(lg[k].grad, lc[k].grad, torch.float32, "d" + k)
+
+
+def test_in_proj_split_weight_gradient_matches_autograd():
+    """InProjFn (mamba_forward's in_proj) against autograd's F.linear, fp32 and bf16 autocast,
+    at T = 4096 tokens so the weight gradient takes the split path."""
+    from s6scan.mamba_inner import InProjFn
+    g = torch.Generator().manual_seed(31)
+    h = torch.randn(4096, 48, generator=g).to(DEV)
+    w = (torch.randn(96, 48, generator=g) * 0.1).to(DEV)
+    bias = (torch.randn(96, generator=g) * 0.1).to(DEV)
+    dy = torch.randn(4096, 96, generator=g).to(DEV)
+    for ac in (False, True):
+        leaves = [t.clone().requires_grad_(True) for t in (h, w, bias)]
+        refs = [t.clone().requires_grad_(True) for t in (h, w, bias)]
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=ac):
+            out = InProjFn.apply(*leaves)
+            ref = torch.nn.functional.linear(*refs)
+        assert out.dtype == ref.dtype
+        out.backward(dy.to(out.dtype))
+        ref.backward(dy.to(ref.dtype))
+        for a, b, name in zip(leaves, refs, ("dh", "dw", "db")):
+            assert a.grad.dtype == b.grad.dtype, name
+            tol = 1e-5 if not ac else 1e-2
+            err = ((a.grad - b.grad).float().norm() / b.grad.float().norm()).item()
+            assert err <= tol, (name, ac, err)
