@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define S6_ABI_VERSION 4
+#define S6_ABI_VERSION 5
 #define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
 #define S6_MAX_DSTATE_BWD 64

@@ -66,6 +66,14 @@ typedef struct S6SsdFwdArgs {
    * after the chunk-scan kernel, so a caller can time that kernel alone.  No counterpart in
    * the reference; it exists for roofline measurement. */
   void* kernel_events[2];
+  /* Optional per-sequence final states (return_varlen_states; replaces chunk_state_varlen,
+   * ssd_chunk_state.py:884-910): with batch == 1 and cu_seqlens [nseq + 1] int32 (device) the
+   * state at the end of each sequence cu_seqlens[i] .. cu_seqlens[i + 1] - 1 is written to
+   * varlen_states [nseq, nheads, headdim, dstate] contiguous, io_dtype.  The carried part
+   * comes from the passed states, so seq_idx should mark the same boundaries.  Sequences
+   * whose bounds are not 0 <= start < end <= seqlen get a zero state.  NULL = off. */
+  const int32_t* cu_seqlens;   int64_t nseq;
+  void* varlen_states;
 } S6SsdFwdArgs;
 
 typedef struct S6SsdBwdArgs {

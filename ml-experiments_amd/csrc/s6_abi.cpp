@@ -461,6 +461,15 @@ int s6_ssd_validate_fwd(const S6SsdFwdArgs* a) {
       ((r = check_strides(a->out_x_stride, 4, "out_x")) ||
        (r = ssd_check_rows(a->out_x, a->out_x_stride, es, "out_x"))))
     return r;
+  if (a->varlen_states != nullptr) {
+    if (p.batch != 1)
+      return fail(S6_E_INVALID, "ssd: varlen states need batch 1, got %lld", (long long)p.batch);
+    if (a->cu_seqlens == nullptr || a->nseq < 1)
+      return fail(S6_E_INVALID, "ssd: varlen states need cu_seqlens with at least one sequence");
+    if (a->nseq > 65535) return fail(S6_E_UNSUPPORTED, "ssd: at most 65535 varlen sequences");
+    if ((uintptr_t)a->varlen_states % 16 != 0)
+      return fail(S6_E_INVALID, "ssd: varlen_states must be 16-byte aligned");
+  }
   const SsdPlan pl = ssd_plan(p);
   if (a->workspace == nullptr || a->workspace_bytes < pl.total)
     return fail(S6_E_WORKSPACE, "ssd forward workspace needs %zu bytes, got %zu", pl.total,
@@ -592,6 +601,7 @@ s6::SsdK ssd_fill(const S6SsdFwdArgs& a0, const SsdPlan& pl) {
   k.init = p.has_initial_states ? a->initial_states : nullptr;
   k.seq = p.has_seq_idx ? a->seq_idx : nullptr;
   k.out = a->out; k.out_x = p.has_z ? a->out_x : nullptr; k.final_states = a->final_states;
+  k.cu = a->cu_seqlens; k.nseq = a->varlen_states ? a->nseq : 0; k.vst = a->varlen_states;
   for (int i = 0; i < 4; ++i) {
     k.sx[i] = a->x_stride[i]; k.sB[i] = a->B_stride[i]; k.sC[i] = a->C_stride[i];
     k.sz[i] = p.has_z ? a->z_stride[i] : 0; k.sout[i] = a->out_stride[i];

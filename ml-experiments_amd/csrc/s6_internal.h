@@ -151,6 +151,8 @@ struct SsdK {
   float* st;    // [Bsz, K, H, P, N] chunk states
   void* hs;     // [Bsz, K, H, P, N] state entering each chunk (io dtype)
   float* cb;    // [Bsz, K, G, Q, Q] C B^T within each chunk (lower-triangle tiles written)
+  const int32_t* cu; int64_t nseq;    // varlen states: sequence bounds (batch 1)
+  void* vst;                          // [nseq, H, P, N] io dtype; NULL: not written
   // ---- backward only ----
   const void* dout; int64_t sdout[4];
   const void* dy; int64_t sdy[4];     // dout * silu(z) (workspace) or dout itself

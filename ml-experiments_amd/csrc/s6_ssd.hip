@@ -76,6 +76,10 @@ __global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
 // MODE 0 (forward): st_c = sum_l x_l (dt'_l e^{S_last - S_l} [seq_l == seq_last]) B_l^T.
 // MODE 1 (backward): dhl_c = sum_l dy_l (e^{S_l} [seq_l == seq before the chunk]) C_l^T,
 // the gradient of the state entering chunk c from the chunk's own outputs.
+// MODE 2 (varlen states, batch 1; chunk_state_varlen, ssd_chunk_state.py:589-660): for the
+// sequence [start, end) and c the chunk of step end - 1, with e = end - 1 - c Q,
+// state = sum_{l in c, l >= start} x_l (dt'_l e^{S_e - S_l}) B_l^T (+ e^{S_e} H_c when the
+// sequence began before chunk c), written in the input type.
 //
 // Software pipeline over 32-step slices: the global loads of slice i + 1 (x rows, B rows and
 // their weights) go to registers while the MFMAs of slice i run; the registers are written,
@@ -104,22 +108,39 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
   Raw (*xr)[kKs][XPT] = reinterpret_cast<Raw (*)[kKs][XPT]>(smem);
   Raw (*br)[kKs][BPT] = reinterpret_cast<Raw (*)[kKs][BPT]>(smem + NB * kKs * XPT * ES);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // work id -> (head fastest, chunk, batch): the heads of one chunk share its B (C) rows
+  // work id -> (head fastest, chunk, batch): the heads of one chunk share its B (C) rows;
+  // MODE 2: (head fastest, sequence)
   const int64_t wid = xcd_work_id();
-  const int64_t hh = wid % k.H, c = (wid / k.H) % k.K, b = wid / (k.H * k.K);
+  const int64_t hh = wid % k.H;
+  int64_t c, b;
+  int lim, rstart = 0;        // rows [rstart, lim) of the chunk contribute
+  bool carry = false;         // MODE 2: add the decayed entering state
+  if constexpr (MODE == 2) {
+    const int64_t si = wid / k.H;
+    const int64_t s0 = k.cu[si], s1 = k.cu[si + 1];
+    const bool ok = 0 <= s0 && s0 < s1 && s1 <= k.L;
+    b = 0;
+    c = ok ? (s1 - 1) / k.Q : 0;
+    lim = ok ? (int)(s1 - c * k.Q) : 0;
+    rstart = ok ? (int)max(s0 - c * k.Q, (int64_t)0) : 0;
+    carry = ok && s0 < c * k.Q;
+  } else {
+    c = (wid / k.H) % k.K;
+    b = wid / (k.H * k.K);
+    lim = (int)min(k.Q, k.L - c * k.Q);
+  }
   const int64_t g = hh / k.hpg;
   const int64_t t0 = c * k.Q;
-  const int lim = (int)min(k.Q, k.L - t0);
   const float* sq = k.dacs + ((b * k.H + hh) * k.K + c) * k.Q;
   const float* dq = k.dtq + ((b * k.H + hh) * k.K + c) * k.Q;
-  const float s_last = sq[k.Q - 1];
-  const int32_t seq_ref = !k.has_seq ? 0
+  const float s_last = MODE == 2 ? (lim > 0 ? sq[lim - 1] : 0.f) : sq[k.Q - 1];
+  const int32_t seq_ref = (!k.has_seq || MODE == 2) ? 0
                           : MODE == 0 ? seq_at(k, b, t0 + lim - 1)
                                       : (c > 0 ? seq_at(k, b, t0 - 1) : 0);
-  const int64_t* sxr = MODE == 0 ? k.sx : k.sdy;
-  const int64_t* sbr = MODE == 0 ? k.sB : k.sC;
-  const char* xbase = (const char*)(MODE == 0 ? k.x : k.dy) + (b * sxr[0] + t0 * sxr[1] + hh * sxr[2]) * ES;
-  const char* bbase = (const char*)(MODE == 0 ? k.Bm : k.Cm) + (b * sbr[0] + t0 * sbr[1] + g * sbr[2]) * ES;
+  const int64_t* sxr = MODE != 1 ? k.sx : k.sdy;
+  const int64_t* sbr = MODE != 1 ? k.sB : k.sC;
+  const char* xbase = (const char*)(MODE != 1 ? k.x : k.dy) + (b * sxr[0] + t0 * sxr[1] + hh * sxr[2]) * ES;
+  const char* bbase = (const char*)(MODE != 1 ? k.Bm : k.Cm) + (b * sbr[0] + t0 * sbr[1] + g * sbr[2]) * ES;
 
   Raw xv[XL][VE], bv[BL][VE];
   float wv[BL];
@@ -142,8 +163,8 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       wv[i] = 0.f;
       if (e < BC && l < lim) {
         load16<T>(bbase + (l * sbr[1] + col) * ES, bv[i]);
-        wv[i] = MODE == 0 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
-        if (k.has_seq && seq_at(k, b, t0 + l) != seq_ref) wv[i] = 0.f;
+        wv[i] = MODE != 1 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
+        if (MODE == 2 ? l < rstart : (k.has_seq && seq_at(k, b, t0 + l) != seq_ref)) wv[i] = 0.f;
       } else {
 #pragma unroll
         for (int q = 0; q < VE; ++q) bv[i][q] = M::to_raw(0.f);
@@ -208,15 +229,34 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
       }
     }
   }
-  float* out = (MODE == 0 ? k.st : k.dhl) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+  if constexpr (MODE == 2) {
+    const Raw* hin = (const Raw*)k.hs + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+    const float sc = carry ? exp_split(s_last) : 0.f;
+    Raw* out = (Raw*)k.vst + ((wid / k.H) * k.H + hh) * (int64_t)(P * N);
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int ti = w + 4 * i;
-    if (ti < NT) {
-      const int pt = ti / NTN, nt = ti % NTN;
+    for (int i = 0; i < TPW; ++i) {
+      const int ti = w + 4 * i;
+      if (ti < NT) {
+        const int pt = ti / NTN, nt = ti % NTN;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        out[(pt * 16 + 4 * (lane >> 4) + j) * N + nt * 16 + (lane & 15)] = acc[i][j];
+        for (int j = 0; j < 4; ++j) {
+          const int o = (pt * 16 + 4 * (lane >> 4) + j) * N + nt * 16 + (lane & 15);
+          const float v = carry ? fmaf(M::from_raw(hin[o]), sc, acc[i][j]) : acc[i][j];
+          out[o] = M::to_raw(v);
+        }
+      }
+    }
+  } else {
+    float* out = (MODE == 0 ? k.st : k.dhl) + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int ti = w + 4 * i;
+      if (ti < NT) {
+        const int pt = ti / NTN, nt = ti % NTN;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          out[(pt * 16 + 4 * (lane >> 4) + j) * N + nt * 16 + (lane & 15)] = acc[i][j];
+      }
     }
   }
 }
@@ -590,6 +630,12 @@ hipError_t ssd_scan_pn(const SsdK& k, hipStream_t st) {
 }
 
 template <typename T, int P, int N>
+hipError_t ssd_varlen_pn(const SsdK& k, hipStream_t st) {
+  hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 2>), dim3((unsigned)(k.nseq * k.H)), dim3(kThreads), 0, st, k);
+  return hipGetLastError();
+}
+
+template <typename T, int P, int N>
 hipError_t ssd_dstates_pn(const SsdK& k, hipStream_t st) {
   hipLaunchKernelGGL((ssd_chunk_state<T, P, N, 1>), dim3((unsigned)(k.K * k.H * k.Bsz)),
                      dim3(kThreads), 0, st, k);
@@ -626,6 +672,7 @@ hipError_t ssd_dstates_pn(const SsdK& k, hipStream_t st) {
 S6_SSD_DISPATCH(ssd_prep)
 S6_SSD_DISPATCH(ssd_scan)
 S6_SSD_DISPATCH(ssd_dstates)
+S6_SSD_DISPATCH(ssd_varlen)
 
 }  // namespace
 
@@ -637,7 +684,8 @@ hipError_t launch_ssd_fwd(const SsdK& k, hipStream_t st, void* const* ev) {
   hipError_t e = ssd_prep(k, st);
   if (e != hipSuccess || (e = record_event(ev, 0, st)) != hipSuccess) return e;
   if ((e = ssd_scan(k, st)) != hipSuccess) return e;
-  return record_event(ev, 1, st);
+  if ((e = record_event(ev, 1, st)) != hipSuccess) return e;
+  return k.vst != nullptr ? ssd_varlen(k, st) : hipSuccess;
 }
 
 }  // namespace s6

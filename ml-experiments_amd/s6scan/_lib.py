@@ -15,7 +15,7 @@ import os
 
 import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 64
@@ -166,6 +166,8 @@ class S6SsdFwdArgs(ctypes.Structure):
         ("final_states", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("kernel_events", _vp * 2),
+        ("cu_seqlens", _vp), ("nseq", _i64),
+        ("varlen_states", _vp),
     ]
 
 

@@ -111,9 +111,11 @@ def _fill_inputs(a, x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx):
 
 def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initial_states=None,
                 seq_idx=None, dt_softplus=False, dt_limit=(0.0, float("inf")),
-                want_final_states=False, want_out_x=False, kernel_events=None):
-    """One forward launch sequence.  Returns (out, out_x, final_states); out_x (the output
-    before the z gate) only with z and ``want_out_x``, final_states only when asked.
+                want_final_states=False, want_out_x=False, kernel_events=None, cu_seqlens=None):
+    """One forward launch sequence.  Returns (out, out_x, final_states, varlen_states); out_x
+    (the output before the z gate) only with z and ``want_out_x``, final_states only when
+    asked, varlen_states [nseq, nheads, headdim, dstate] (x's dtype) only with
+    ``cu_seqlens`` (batch 1; chunk_state_varlen, ssd_chunk_state.py:884-910).
     ``kernel_events``: optional pair of torch.cuda.Events that the library records right
     before and after its chunk-scan kernel (measurement only)."""
     batch, seqlen, nheads, headdim = x.shape
@@ -133,6 +135,12 @@ def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initia
         a.out, a.out_stride = _ptr(out), _st(out, 4)
         a.out_x, a.out_x_stride = _ptr(out_x), _st(out_x, 4)
         a.final_states = _ptr(final)
+        varlen = None
+        if cu_seqlens is not None:
+            cu = cu_seqlens.to(device=x.device, dtype=torch.int32).contiguous()
+            varlen = torch.empty(cu.numel() - 1, nheads, headdim, dstate, dtype=dtype,
+                                 device=x.device)
+            a.cu_seqlens, a.nseq, a.varlen_states = _ptr(cu), cu.numel() - 1, _ptr(varlen)
         nbytes = _lib.LIB.s6_ssd_fwd_workspace_bytes(ctypes.byref(a.p))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
         a.workspace, a.workspace_bytes = _ptr(ws), nbytes
@@ -140,7 +148,7 @@ def ssd_forward(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None, initia
             a.kernel_events[0], a.kernel_events[1] = (e.cuda_event for e in kernel_events)
         stream = torch.cuda.current_stream(x.device).cuda_stream
         _lib.check(_lib.LIB.s6_ssd_fwd(ctypes.byref(a), ctypes.c_void_p(stream)), "s6_ssd_fwd")
-    return out, out_x, final
+    return out, out_x, final, varlen
 
 
 def ssd_backward(dout, x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
@@ -207,20 +215,29 @@ class MambaChunkScanCombinedFn(torch.autograd.Function):
                 initial_states=None, seq_idx=None, cu_seqlens=None, dt_softplus=False,
                 dt_limit=(0.0, float("inf")), return_final_states=False,
                 return_varlen_states=False):
-        if cu_seqlens is not None or return_varlen_states:
-            raise NotImplementedError("mamba_chunk_scan_combined: varlen states are not built yet")
-        out, out_x, final = ssd_forward(x, dt, A, B, C, chunk_size, D=D, z=z, dt_bias=dt_bias,
-                                        initial_states=initial_states, seq_idx=seq_idx,
-                                        dt_softplus=dt_softplus, dt_limit=dt_limit,
-                                        want_final_states=return_final_states,
-                                        want_out_x=z is not None)
+        # the reference's argument rules (ssd_combined.py:537-540, 329)
+        if not return_varlen_states:
+            cu_seqlens = None
+        else:
+            assert cu_seqlens is not None, "cu_seqlens must be provided if return_varlen_states is True"
+            assert x.shape[0] == 1, \
+                "passing cu_seqlens to get the varlen states is only supported if batch dimension is 1"
+        out, out_x, final, varlen = ssd_forward(
+            x, dt, A, B, C, chunk_size, D=D, z=z, dt_bias=dt_bias, initial_states=initial_states,
+            seq_idx=seq_idx, dt_softplus=dt_softplus, dt_limit=dt_limit,
+            want_final_states=return_final_states, want_out_x=z is not None,
+            cu_seqlens=cu_seqlens)
         ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, out_x)
         ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit = chunk_size, dt_softplus, dt_limit
         ctx.return_final_states = return_final_states
-        return out if not return_final_states else (out, final)
+        ctx.return_varlen_states = return_varlen_states
+        if not return_varlen_states:
+            return out if not return_final_states else (out, final)
+        return (out, varlen) if not return_final_states else (out, final, varlen)
 
     @staticmethod
     def backward(ctx, dout, *args):
+        assert not ctx.return_varlen_states, "return_varlen_states is not supported in backward"
         x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, out_x = ctx.saved_tensors
         dfinal = args[0] if ctx.return_final_states else None
         dx, ddt, dA, dB, dC, dD, dz, dbias, dinit = ssd_backward(

@@ -19,6 +19,9 @@ step by step, with the semantics of each Triton kernel it calls:
   first chunk)] + sum_{s<=l} CB[l,s] e^{S_l - S_s} dt'_s x_s + D x_l; out = y silu(z)
                                                             (ssd_chunk_scan.py:43-185)
 
+``ssd_varlen_states_ref`` restates the per-sequence final states of a packed batch-1 input
+(chunk_state_varlen); tests pin it against the brute force on each sequence's prefix.
+
 ``ssd_brute64`` is an independent float64 NumPy loop over the recurrence itself (state reset
 where seq_idx changes, the initial state belonging to seq_idx 0).  Tests
 (``tests/test_oracle_ssd.py``) pin the chunked restatement against it, and the brute force
@@ -40,11 +43,10 @@ def _dt_process(dt, dt_bias, dt_softplus, dt_limit):
     return dt.clamp(min=dt_limit[0], max=dt_limit[1])
 
 
-def ssd_chunked_ref(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
-                    initial_states=None, seq_idx=None, dt_softplus=False,
-                    dt_limit=(0.0, float("inf")), compute_dtype=torch.float32):
-    """Returns (out, out_x, final_states); out_x is y before the z gate (None without z)."""
-    cd = compute_dtype
+def _chunked_states(x, dt, A, B, chunk_size, dt_bias, initial_states, seq_idx, dt_softplus,
+                    dt_limit, cd):
+    """The chunk quantities shared by the forward and the varlen states: processed dt, the
+    per-chunk cumsum S, the chunk states and the states entering each chunk."""
     batch, L, H, P = x.shape
     G, N = B.shape[2], B.shape[3]
     hpg = H // G
@@ -52,13 +54,12 @@ def ssd_chunked_ref(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
     K = math.ceil(L / Q)
     pad = K * Q - L
     f = lambda t: None if t is None else t.to(cd)
-    x, dt, B, C, z = f(x), f(dt), f(B), f(C), f(z)
+    x, dt, B = f(x), f(dt), f(B)
     dtp = _dt_process(dt, f(dt_bias), dt_softplus, dt_limit)            # (b, L, h)
     padL = lambda t: F.pad(t, (0, 0) * (t.dim() - 2) + (0, pad)) if pad else t
     dtp = padL(dtp)                                                      # zero past the end
     xc = padL(x).reshape(batch, K, Q, H, P)
     Bh = padL(B).repeat_interleave(hpg, dim=2).reshape(batch, K, Q, H, N)
-    Ch = padL(C).repeat_interleave(hpg, dim=2).reshape(batch, K, Q, H, N)
     dtc = dtp.reshape(batch, K, Q, H)
     S = torch.cumsum(dtc * f(A), dim=2)                                  # (b, K, Q, h)
     if seq_idx is not None:
@@ -84,6 +85,26 @@ def ssd_chunked_ref(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
         Hc = scale[:, :, None, None] * Hc + st[:, c]
     final = Hc
     Hs = torch.stack(Hs, dim=1)                                          # (b, K, h, p, n)
+    return dict(x=x, dtp=dtp, xc=xc, Bh=Bh, dtc=dtc, S=S, Hs=Hs, final=final,
+                seqp=seqp if seq_idx is not None else None, K=K, Q=Q, pad=pad, hpg=hpg)
+
+
+def ssd_chunked_ref(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                    initial_states=None, seq_idx=None, dt_softplus=False,
+                    dt_limit=(0.0, float("inf")), compute_dtype=torch.float32):
+    """Returns (out, out_x, final_states); out_x is y before the z gate (None without z)."""
+    cd = compute_dtype
+    f = lambda t: None if t is None else t.to(cd)
+    q = _chunked_states(x, dt, A, B, chunk_size, dt_bias, initial_states, seq_idx, dt_softplus,
+                        dt_limit, cd)
+    x, xc, Bh, dtc, S, Hs, final = q["x"], q["xc"], q["Bh"], q["dtc"], q["S"], q["Hs"], q["final"]
+    K, Q, pad, hpg = q["K"], q["Q"], q["pad"], q["hpg"]
+    seqp = q["seqp"]
+    batch, L, H, P = x.shape
+    N = B.shape[3]
+    padL = lambda t: F.pad(t, (0, 0) * (t.dim() - 2) + (0, pad)) if pad else t
+    Ch = padL(f(C)).repeat_interleave(hpg, dim=2).reshape(batch, K, Q, H, N)
+    z = f(z)
     # C B^T within chunks, decay, causal mask
     CB = torch.einsum("bclhn,bcshn->bchls", Ch, Bh)
     if seq_idx is not None:
@@ -109,6 +130,32 @@ def ssd_chunked_ref(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
         out_x = y
         y = y * F.silu(z)
     return y, out_x, final
+
+
+def ssd_varlen_states_ref(x, dt, A, B, chunk_size, cu_seqlens, dt_bias=None,
+                          initial_states=None, seq_idx=None, dt_softplus=False,
+                          dt_limit=(0.0, float("inf")), compute_dtype=torch.float32):
+    """The state at the end of each sequence of a packed batch-1 input, as the reference's
+    chunk_state_varlen computes it (ssd_chunk_state.py:589-660, called at
+    ssd_combined.py:329-331): for the sequence [s0, s1) and c the chunk of step s1 - 1,
+    the chunk-state sum over the rows of chunk c from max(s0, c Q) to s1 - 1 with the decay
+    to step s1 - 1, plus e^{S(s1 - 1)} times the state entering chunk c when s0 < c Q.
+    Returns [nseq, nheads, headdim, dstate]."""
+    q = _chunked_states(x, dt, A, B, chunk_size, dt_bias, initial_states, seq_idx, dt_softplus,
+                        dt_limit, compute_dtype)
+    xc, Bh, dtc, S, Hs, Q = q["xc"], q["Bh"], q["dtc"], q["S"], q["Hs"], q["Q"]
+    cu = [int(v) for v in cu_seqlens]
+    out = []
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        c = (s1 - 1) // Q
+        e = s1 - 1 - c * Q
+        r0 = max(s0 - c * Q, 0)
+        w = dtc[0, c, r0:e + 1] * torch.exp(S[0, c, e][None] - S[0, c, r0:e + 1])   # (rows, h)
+        st = torch.einsum("lhp,lh,lhn->hpn", xc[0, c, r0:e + 1], w, Bh[0, c, r0:e + 1])
+        if s0 < c * Q:
+            st = st + torch.exp(S[0, c, e])[:, None, None] * Hs[0, c]
+        out.append(st)
+    return torch.stack(out)
 
 
 def ssd_brute64(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None,

@@ -72,7 +72,7 @@ def test_ssd_forward_matches_reference(case, dtype):
     batch, L, H, P, G, N, Q, opts = case
     t, kw = make(batch, L, H, P, G, N, dtype, seed=L + N, opts=opts)
     gpu = {k: v.to(DEV) for k, v in t.items()}
-    out, out_x, final = ssd_forward(**gpu, chunk_size=Q, want_final_states=True,
+    out, out_x, final, _ = ssd_forward(**gpu, chunk_size=Q, want_final_states=True,
                                     want_out_x=True, **kw)
     ref, ref_x, ref_final = ssd_chunked_ref(**t, chunk_size=Q, compute_dtype=torch.float64, **kw)
     assert out.shape == (batch, L, H, P) and out.dtype == dtype
@@ -166,3 +166,53 @@ def test_ssd_backward_is_deterministic():
         grads.append([gpu[k].grad.clone() for k in sorted(gpu)])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+VCU = [0, 50, 64, 200, 201, 513, 700]  # chunk 64: ends on a boundary, carries, length 1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_seq", [True, False])
+def test_ssd_varlen_states_match_reference(dtype, with_seq):
+    from oracle.ssd_ref import ssd_varlen_states_ref
+    t, kw = make(1, 700, 3, 32, 1, 32, dtype, seed=77, opts=("bias", "D", "init"))
+    seq = torch.zeros(1, 700, dtype=torch.int32)
+    for i, (s0, s1) in enumerate(zip(VCU[:-1], VCU[1:])):
+        seq[0, s0:s1] = i
+    if with_seq:
+        t["seq_idx"] = seq
+    gpu = {k: v.to(DEV) for k, v in t.items()}
+    out, final, vst = mamba_chunk_scan_combined(
+        **gpu, chunk_size=64, cu_seqlens=torch.tensor(VCU, dtype=torch.int32, device=DEV),
+        return_final_states=True, return_varlen_states=True, **kw)
+    assert vst.shape == (len(VCU) - 1, 3, 32, 32) and vst.dtype == dtype
+    ref = ssd_varlen_states_ref(t["x"].double(), t["dt"].double(), t["A"].double(),
+                                t["B"].double(), 64, torch.tensor(VCU),
+                                dt_bias=t["dt_bias"].double(),
+                                initial_states=t["initial_states"].double(),
+                                seq_idx=t.get("seq_idx"), compute_dtype=torch.float64, **kw)
+    check(vst, ref, dtype, "varlen_states")
+    # the last sequence ends at the end of the input: its state is the final state
+    if with_seq:
+        check(final[0].float(), ref[-1], torch.float32 if dtype == torch.float32 else dtype, "final")
+
+
+def test_ssd_varlen_states_argument_rules():
+    """The reference's asserts (ssd_combined.py:329, 540, 557)."""
+    t, kw = make(2, 128, 2, 32, 1, 32, torch.float32, seed=5)
+    gpu = {k: v.to(DEV) for k, v in t.items()}
+    cu = torch.tensor([0, 100, 128], dtype=torch.int32, device=DEV)
+    with pytest.raises(AssertionError, match="batch dimension is 1"):
+        mamba_chunk_scan_combined(**gpu, chunk_size=64, cu_seqlens=cu, return_varlen_states=True, **kw)
+    one = {k: v[:1].contiguous() for k, v in gpu.items() if k != "A"}
+    one["A"] = gpu["A"]
+    with pytest.raises(AssertionError, match="cu_seqlens must be provided"):
+        mamba_chunk_scan_combined(**one, chunk_size=64, return_varlen_states=True, **kw)
+    # cu_seqlens without return_varlen_states is ignored, as in the reference
+    out = mamba_chunk_scan_combined(**one, chunk_size=64, cu_seqlens=cu, **kw)
+    assert torch.is_tensor(out)
+    x = one["x"].clone().requires_grad_(True)
+    out, vst = mamba_chunk_scan_combined(**dict(one, x=x), chunk_size=64, cu_seqlens=cu,
+                                         return_varlen_states=True, **kw)
+    with pytest.raises(AssertionError, match="not supported in backward"):
+        out.sum().backward()

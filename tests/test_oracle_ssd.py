@@ -56,3 +56,44 @@ def test_chunked_restatement_matches_brute_force(chunk, opts):
     want, want_final = ssd_brute64(**t, **kw)
     np.testing.assert_allclose(out.numpy(), want, rtol=1e-10, atol=1e-10)
     np.testing.assert_allclose(final.numpy(), want_final, rtol=1e-10, atol=1e-10)
+
+
+CU = [0, 9, 16, 27, 45, 46, 61]   # chunk 8: ends on a boundary (16), spans chunks (27, 45), length 1
+
+
+@pytest.mark.parametrize("with_seq", [True, False])
+@pytest.mark.parametrize("init", [False, True])
+def test_varlen_states_match_the_brute_force_on_each_prefix(with_seq, init):
+    """chunk_state_varlen's states, pinned without its own formula:
+    * with seq_idx marking the sequences, each is the brute-force state of that sequence
+      run alone (the first one from initial_states);
+    * without it, a sequence that starts inside its last chunk still gets only its own rows,
+      and one that starts earlier gets the unsegmented state at its end (the carried part
+      holds the whole history)."""
+    from oracle.ssd_ref import ssd_varlen_states_ref
+    t = inputs(batch=1, L=61, seed=11)
+    for k in ("z", "D", "C"):
+        t.pop(k)
+    Q = 8
+    seq = torch.zeros(1, 61, dtype=torch.int32)
+    for i, (s0, s1) in enumerate(zip(CU[:-1], CU[1:])):
+        seq[0, s0:s1] = i
+    init_st = (torch.randn(1, 4, 3, 5, generator=torch.Generator().manual_seed(2), dtype=torch.float64)
+               if init else None)
+    got = ssd_varlen_states_ref(**t, chunk_size=Q, cu_seqlens=torch.tensor(CU),
+                                initial_states=init_st, seq_idx=seq if with_seq else None,
+                                dt_softplus=True, compute_dtype=torch.float64)
+    assert got.shape == (len(CU) - 1, 4, 3, 5)
+    Cd = torch.zeros(1, 61, 2, 5, dtype=torch.float64)
+    for i, (s0, s1) in enumerate(zip(CU[:-1], CU[1:])):
+        sl = lambda v: v[:, s0:s1]
+        if with_seq or s0 >= (s1 - 1) // Q * Q:
+            first = i == 0
+            _, want = ssd_brute64(sl(t["x"]), sl(t["dt"]), t["A"], sl(t["B"]), sl(Cd),
+                                  dt_bias=t["dt_bias"], dt_softplus=True,
+                                  initial_states=init_st if (first and (with_seq or s0 == 0)) else None)
+        else:
+            pre = lambda v: v[:, :s1]
+            _, want = ssd_brute64(pre(t["x"]), pre(t["dt"]), t["A"], pre(t["B"]), pre(Cd),
+                                  dt_bias=t["dt_bias"], dt_softplus=True, initial_states=init_st)
+        np.testing.assert_allclose(got[i].numpy(), want[0], rtol=1e-10, atol=1e-10, err_msg=f"seq {i}")
