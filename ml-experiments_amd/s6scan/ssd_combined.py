@@ -8,12 +8,15 @@ ssd_combined.py:563-582, forward :281-332):
                               initial_states=None, seq_idx=None, cu_seqlens=None,
                               dt_softplus=False, dt_limit=(0.0, inf),
                               return_final_states=False, return_varlen_states=False)
-        -> out | (out, final_states)
+        -> out | (out, final_states) | (out, varlen_states) | (out, final_states, varlen_states)
 
 * x, z: (batch, seqlen, nheads, headdim); dt: (batch, seqlen, nheads); A, dt_bias:
   (nheads,); B, C: (batch, seqlen, ngroups, dstate); D: (nheads,) or (nheads, headdim);
   initial_states: (batch, nheads, headdim, dstate); seq_idx: (batch, seqlen) int32.
 * out has x's dtype (bf16 or fp32); final_states is fp32 (batch, nheads, headdim, dstate).
+* return_varlen_states (batch 1, cu_seqlens int32 (nseq + 1,)): the state at the end of each
+  packed sequence, (nseq, nheads, headdim, dstate) in x's dtype, forward only, as the
+  reference's chunk_state_varlen (ssd_chunk_state.py:884-910).
 
 The forward runs five HIP kernels (chunk cumsum, chunk states and C B^T on MFMA, state
 passing, the chunk scan on MFMA; ml-experiments_amd/csrc/s6_ssd.hip); the backward recomputes
