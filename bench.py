@@ -22,6 +22,8 @@ Mamba-2 SSD (mamba_chunk_scan_combined) forward and forward + backward at Mamba-
 * cpu_baseline: the CPU restatement of the reference path (selective_scan_ref, op for op,
   oracle/selective_scan_ref.py) timed on the host cores on a bounded sample of the same
   workload.
+* fwd_bwd (fwd1 only, unless --no-fwdbwd): the config-3 training-shape forward + backward
+  measured the same way, since the metric covers both; ``value`` stays the forward's.
 Only one GPU is used: --gpus above 1 exits with a message.
 """
 import argparse
@@ -53,6 +55,8 @@ def parse():
                     choices=["fwd1", "fwdbwd3", "fwd2", "fwdbwd4", "mixer1", "mamba3",
                              "decode", "ssd2", "copyref"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fwdbwd", action="store_true",
+                    help="fwd1 only: skip the config-3 fwd+bwd measurement carried in its line")
     return ap.parse_args()
 
 
@@ -497,35 +501,15 @@ def copy_reference(torch, steps):
                       "bytes_written_per_launch": 4 * n, "launches": max(steps, 1)}))
 
 
-def main():
-    args = parse()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, "
-              f"WORLD_SIZE {world}); the scan shards over batch/channels without "
-              "communication, so run it per GPU.", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    if args.workload == "copyref":
-        copy_reference(torch, args.steps)
-        return
-    import s6scan
-    if args.workload == "mamba3":
-        run_mamba(torch, args)
-        return
-    if args.workload == "decode":
-        run_decode(torch, args)
-        return
-    if args.workload == "ssd2":
-        run_ssd(torch, args)
-        return
+def measure_scan(torch, workload, steps, warmup):
+    """One of the scan workloads (fwd1, fwdbwd3, fwd2, fwdbwd4, mixer1): its bench dict,
+    without the CPU baseline."""
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
 
     cfg = {"fwd1": CONFIGS[1], "fwdbwd3": CONFIGS[3], "fwd2": CONFIGS[2],
-           "fwdbwd4": CONFIGS[4], "mixer1": CONFIGS[1]}[args.workload]
-    mixer = args.workload == "mixer1"
+           "fwdbwd4": CONFIGS[4], "mixer1": CONFIGS[1]}[workload]
+    mixer = workload == "mixer1"
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
@@ -565,11 +549,11 @@ def main():
             selective_scan_backward(*a, g["D"], None, None, False, g["dy"].mT, xck, cu_seqlens=cu,
                                     kernel_events=ev_b)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
 
-    K = args.steps
+    K = steps
     mk = lambda: torch.cuda.Event(enable_timing=True)
     evs = [(mk(), mk()) for _ in range(K)]
     evs_b = [(mk(), mk()) for _ in range(K)] if cfg.backward else [None] * K
@@ -606,7 +590,7 @@ def main():
     traffic = valu_busy = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            prof = json.load(f).get(args.workload)
+            prof = json.load(f).get(workload)
         if prof:
             traffic = round(prof["traffic_bytes_per_launch"])
             valu_busy = round(prof["kernels"][prof["dominant_kernel"]]["valu_busy"], 3)
@@ -616,7 +600,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": K,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -649,9 +633,47 @@ def main():
     }
     if cfg.backward:
         res["fwd_kernel_ms"] = round(k_ms, 5)
+    return res
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); the scan shards over batch/channels without "
+              "communication, so run it per GPU.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if args.workload == "copyref":
+        copy_reference(torch, args.steps)
+        return
+    import s6scan
+    if args.workload == "mamba3":
+        run_mamba(torch, args)
+        return
+    if args.workload == "decode":
+        run_decode(torch, args)
+        return
+    if args.workload == "ssd2":
+        run_ssd(torch, args)
+        return
+    res = measure_scan(torch, args.workload, args.steps, args.warmup)
+    if args.workload == "fwd1" and not args.no_fwdbwd:
+        # BASELINE's metric covers fwd and fwd+bwd: the training-shape fwd+bwd (config 3)
+        # rides along, measured the same way; value stays the config-1 forward.
+        log("fwd+bwd (config 3) ...")
+        fb = measure_scan(torch, "fwdbwd3", max(10, args.steps // 2), max(3, args.warmup // 2))
+        res["fwd_bwd"] = {k: fb[k] for k in ("value", "unit", "ms_per_step", "hbm_frac",
+                                              "mtok_ch_per_s", "steps", "config", "roofline",
+                                              "fwd_kernel_ms")}
     if not args.no_cpu_baseline:
+        from s6scan.configs import CONFIGS, make_inputs
         log("cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(cfg, make_inputs, mixer=mixer)
+        cfg = {"fwd1": CONFIGS[1], "fwdbwd3": CONFIGS[3], "fwd2": CONFIGS[2],
+               "fwdbwd4": CONFIGS[4], "mixer1": CONFIGS[1]}[args.workload]
+        res["cpu_baseline"] = cpu_baseline(cfg, make_inputs, mixer=args.workload == "mixer1")
     print(json.dumps(res), flush=True)
 
 
