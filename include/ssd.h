@@ -26,7 +26,7 @@
  * Rows accessed with 16-byte vector loads and stores (x, z, B, C, out, out_x, dout) need a
  * unit last stride and must start on 16-byte boundaries.
  * Supported: headdim in {32, 64, 128}, dstate in {32, 64, 128, 256}, chunk_size in
- * {64, 128, 256}, io_dtype bf16 or fp32.  Errors and streams as in s6scan.h.
+ * {64, 128, 256}, io_dtype bf16, fp16 or fp32.  Errors and streams as in s6scan.h.
  */
 #ifndef S6_SSD_H
 #define S6_SSD_H

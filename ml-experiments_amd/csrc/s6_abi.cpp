@@ -389,8 +389,8 @@ int ssd_check_problem(const S6SsdProblem& p) {
   if (p.chunk_size != 64 && p.chunk_size != 128 && p.chunk_size != 256)
     return fail(S6_E_UNSUPPORTED, "ssd: chunk_size must be 64, 128 or 256, got %lld",
                 (long long)p.chunk_size);
-  if (p.io_dtype != S6_BF16 && p.io_dtype != S6_F32)
-    return fail(S6_E_UNSUPPORTED, "ssd: io dtype must be bf16 or fp32");
+  if (p.io_dtype != S6_BF16 && p.io_dtype != S6_F16 && p.io_dtype != S6_F32)
+    return fail(S6_E_UNSUPPORTED, "ssd: io dtype must be bf16, fp16 or fp32");
   if (ceil_div(p.seqlen, p.chunk_size) > 65535 || p.batch * p.nheads > 65535 || p.batch > 65535)
     return fail(S6_E_UNSUPPORTED, "ssd: too many chunks or batch * nheads above 65535");
   if ((p.chunk_size / 64) * ceil_div(p.seqlen, p.chunk_size) * p.batch * p.nheads >= ((int64_t)1 << 31))

@@ -665,6 +665,7 @@ hipError_t ssd_dstates_pn(const SsdK& k, hipStream_t st) {
   }                                                                                       \
   hipError_t FN(const SsdK& k, hipStream_t st) {                                          \
     if (k.io == S6_BF16) return FN##_t<bf16>(k, st);                                      \
+    if (k.io == S6_F16) return FN##_t<f16>(k, st);                                        \
     if (k.io == S6_F32) return FN##_t<float>(k, st);                                      \
     return hipErrorInvalidValue;                                                          \
   }

@@ -956,6 +956,7 @@ hipError_t launch_ssd_bwd(const SsdK& k, hipStream_t st) {
   hipError_t e = launch_ssd_prep(k, st);
   if (e != hipSuccess) return e;
   if (k.io == S6_BF16) return ssd_bwd_t<bf16>(k, st);
+  if (k.io == S6_F16) return ssd_bwd_t<f16>(k, st);
   if (k.io == S6_F32) return ssd_bwd_t<float>(k, st);
   return hipErrorInvalidValue;
 }

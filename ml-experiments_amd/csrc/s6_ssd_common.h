@@ -2,9 +2,10 @@
 // backward): the MFMA operand abstraction and small helpers.
 //
 // MFMA use.  Every contraction runs on 16x16 output tiles with K = 32 per step: one
-// v_mfma_f32_16x16x32_bf16 for bf16 operands, eight v_mfma_f32_16x16x4_f32 for fp32.
+// v_mfma_f32_16x16x32_bf16 / _f16 for bf16 / fp16 operands, eight v_mfma_f32_16x16x4_f32
+// for fp32.
 // Lane i of a wave holds A[i % 16][k(i, j)] and B[k(i, j)][i % 16] for items j < 8, with
-// k(i, j) = 8 (i / 16) + j (bf16) or i / 16 + 4 j (fp32), and D[4 (i / 16) + j][i % 16]
+// k(i, j) = 8 (i / 16) + j (bf16, fp16) or i / 16 + 4 j (fp32), and D[4 (i / 16) + j][i % 16]
 // for j < 4.
 #pragma once
 #include "s6_internal.h"
@@ -20,8 +21,10 @@ constexpr int kLp = kKs + 8;       // LDS row pitch in elements: 16-byte aligned
 constexpr int kThreads = 256;
 
 template <typename T> struct Mma;
-template <> struct Mma<bf16> {
-  typedef __bf16 Frag __attribute__((ext_vector_type(8)));
+// 16-bit operand types (bf16, fp16): 8 elements of one row per lane, one 16-byte load.
+template <typename E>
+struct Mma16 {
+  typedef E Frag __attribute__((ext_vector_type(8)));
   typedef uint16_t Raw;
   static constexpr int kVe = 8;  // elements per 16-byte load
   __device__ static inline int kidx(int lane, int j) { return 8 * (lane >> 4) + j; }
@@ -49,22 +52,28 @@ template <> struct Mma<bf16> {
   __device__ static inline Frag from_float(const float (&v)[8]) {
     Frag f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<E>(v[j]);
     return f;
   }
   __device__ static inline Frag zero() {
     Frag f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(0.f);
+    for (int j = 0; j < 8; ++j) f[j] = static_cast<E>(0.f);
     return f;
   }
+  __device__ static inline Raw to_raw(float v) { return __builtin_bit_cast(uint16_t, static_cast<E>(v)); }
+  __device__ static inline float from_raw(Raw r) { return static_cast<float>(__builtin_bit_cast(E, r)); }
+};
+template <> struct Mma<bf16> : Mma16<__bf16> {
   __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
   }
-  __device__ static inline Raw to_raw(float v) {
-    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
-  }
   __device__ static inline float from_raw(Raw r) { return __uint_as_float((uint32_t)r << 16); }
+};
+template <> struct Mma<f16> : Mma16<_Float16> {
+  __device__ static inline void mma(f4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+  }
 };
 template <> struct Mma<float> {
   struct Frag { float v[8]; };

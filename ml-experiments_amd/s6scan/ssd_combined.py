@@ -13,7 +13,7 @@ ssd_combined.py:563-582, forward :281-332):
 * x, z: (batch, seqlen, nheads, headdim); dt: (batch, seqlen, nheads); A, dt_bias:
   (nheads,); B, C: (batch, seqlen, ngroups, dstate); D: (nheads,) or (nheads, headdim);
   initial_states: (batch, nheads, headdim, dstate); seq_idx: (batch, seqlen) int32.
-* out has x's dtype (bf16 or fp32); final_states is fp32 (batch, nheads, headdim, dstate).
+* out has x's dtype (bf16, fp16 or fp32); final_states is fp32 (batch, nheads, headdim, dstate).
 * return_varlen_states (batch 1, cu_seqlens int32 (nseq + 1,)): the state at the end of each
   packed sequence, (nseq, nheads, headdim, dstate) in x's dtype, forward only, as the
   reference's chunk_state_varlen (ssd_chunk_state.py:884-910).
@@ -31,7 +31,7 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
 
 def _ptr(t):
@@ -85,7 +85,7 @@ def _prepare(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx):
     if not x.is_cuda:
         raise RuntimeError("mamba_chunk_scan_combined: tensors must be on a ROCm device (no CPU path)")
     if x.dtype not in _DTYPES:
-        raise NotImplementedError(f"mamba_chunk_scan_combined: dtype {x.dtype} (bf16 or fp32 only)")
+        raise NotImplementedError(f"mamba_chunk_scan_combined: dtype {x.dtype} (bf16, fp16 or fp32 only)")
     dtype = x.dtype
     x, B, C = _rows16(x), _rows16(B.to(dtype)), _rows16(C.to(dtype))
     if z is not None:

@@ -45,12 +45,14 @@ def make(batch, L, H, P, G, N, dtype, seed, opts=()):
 def check(out, ref, dtype, what):
     if dtype == torch.float32:
         assert_close(out, ref, 1e-4, 1e-4 * rms(ref), what)
-    else:  # the scaled B, the decayed CB and the passed states are rounded to bf16 (as in the
-        # reference); compare norm-wise and elementwise against the float64 value
+    else:  # the scaled B, the decayed CB and the passed states are rounded to the 16-bit type
+        # (as in the reference); compare norm-wise and elementwise against the float64 value
+        # (fp16 keeps 3 more mantissa bits than bf16, so its bounds are 8x tighter)
+        k = 1.0 if dtype == torch.bfloat16 else 0.125
         d = (out.float().cpu() - ref.float())
         rel = (d.norm() / ref.float().norm()).item()
-        assert rel < 1.5e-2, f"{what}: norm-wise relative error {rel:.3g}"
-        assert_close(out, ref, 5e-2, 5e-2 * rms(ref), what)
+        assert rel < 1.5e-2 * k, f"{what}: norm-wise relative error {rel:.3g}"
+        assert_close(out, ref, 5e-2 * k, 5e-2 * k * rms(ref), what)
 
 
 CASES = [  # batch, L, H, P, G, N, chunk, opts
@@ -66,7 +68,7 @@ CASES = [  # batch, L, H, P, G, N, chunk, opts
 ]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", CASES)
 def test_ssd_forward_matches_reference(case, dtype):
     batch, L, H, P, G, N, Q, opts = case
@@ -127,10 +129,11 @@ def check_grad(a, b, dtype, what):
     else:
         d = a.detach().float().cpu() - b.detach().float()
         rel = (d.norm() / b.detach().float().norm()).item()
-        assert rel < 3e-2, f"{what}: norm-wise relative error {rel:.3g}"
+        bound = 3e-2 if dtype == torch.bfloat16 else 3e-2 / 8
+        assert rel < bound, f"{what}: norm-wise relative error {rel:.3g}"
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", GRAD_CASES)
 def test_ssd_backward_matches_autograd(case, dtype):
     batch, L, H, P, G, N, Q, opts = case
