@@ -60,6 +60,43 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_model():
+    """The host CPU's model name (the survey asks for it next to the CPU baseline)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_config0_one_thread(make_inputs):
+    """Config 0 (the reference's own CPU-runnable case: B=1, L=1024, D=128, N=16, fp32
+    forward) through the restated reference path on 1 thread, median of 3."""
+    import torch
+    from s6scan.configs import CONFIGS
+    from oracle.selective_scan_ref import selective_scan_ref
+    cfg = CONFIGS[0]
+    inp = make_inputs(cfg)
+    args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        selective_scan_ref(*args, D=inp["D"], return_last_state=True)
+        ts = []
+        for _ in range(3):
+            t = time.perf_counter()
+            selective_scan_ref(*args, D=inp["D"], return_last_state=True)
+            ts.append(time.perf_counter() - t)
+    finally:
+        torch.set_num_threads(prev)
+    sec = statistics.median(ts)
+    return {"seconds": round(sec, 4), "GB_per_s": round(cfg.algorithmic_bytes() / sec / 1e9, 5),
+            "threads": 1}
+
+
 def cpu_baseline(cfg, make_inputs, mixer=False):
     """Reference CPU path on a bounded sample: one sequence of the workload (4096 steps
     forward, 2048 steps forward + backward).  The scan workloads time the torch restatement
@@ -104,6 +141,8 @@ def cpu_baseline(cfg, make_inputs, mixer=False):
                    f"{cfg.name}: batch 1, seqlen {seqlen}, dim {cfg.dim}, dstate {cfg.dstate}; "
                    f"median of 3 runs = {sec:.3f} s; os.cpu_count() = {os.cpu_count()}"),
         "mtok_ch_per_s": round(seqlen * cfg.dim / sec / 1e6, 4),
+        "cpu_model": cpu_model(),
+        "config0_one_thread": cpu_config0_one_thread(make_inputs),
     }
 
 
@@ -176,7 +215,7 @@ def mamba_cpu_baseline(torch, cfg):
     sec = statistics.median(ts)
     d_inner = 2 * cfg["d_model"]
     return {"value": round(L * d_inner / sec / 1e6, 4), "unit": "Mtok·ch/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "kind": "port", "cpu_model": cpu_model(),
             "sample": (f"restated reference block (mamba_inner_ref: nn.Conv1d path, "
                        f"selective_scan_ref op for op, autograd backward), fp32, batch 1, "
                        f"seqlen {L}, d_model {cfg['d_model']}; median of 3 runs = {sec:.3f} s")}
@@ -347,7 +386,7 @@ def run_decode(torch, args):
                                            s_["z"], bc, True)
             ts.append((time.perf_counter() - t) * 1e6 / S)
         res["cpu_baseline"] = {"value": round(statistics.median(ts), 3), "unit": "us/step",
-                               "cores": torch.get_num_threads(), "kind": "port",
+                               "cores": torch.get_num_threads(), "kind": "port", "cpu_model": cpu_model(),
                                "sample": f"restated selective_state_update_ref, the full "
                                          f"workload ({S} steps, median of 3 runs)"}
     print(json.dumps(res), flush=True)
@@ -480,7 +519,7 @@ def run_ssd(torch, args):
             reps += 1
         sec = time.perf_counter() - t
         res["cpu_baseline"] = {"value": round(reps * Ls * H * P / sec / 1e6, 4), "unit": "Mtok·ch/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
+                               "cores": torch.get_num_threads(), "kind": "port", "cpu_model": cpu_model(),
                                "sample": (f"restated reference chunked forward (ssd_chunked_ref, "
                                           f"fp32 torch ops), batch 1, seqlen {Ls}, {reps} calls: "
                                           f"{sec:.2f} s")}
