@@ -315,3 +315,31 @@ def test_fwd_bwd_configs_full_size_vs_c_oracle(k):
                          (True, True, False, True, True, False)):
         got = x.grad.mT if tr else x.grad
         assert_grad_close(got, rg[nm], cfg.dtype, nm)
+
+
+def _random_cases(n, seed=20261202):
+    """Seeded random shapes over the supported space: odd dstate, channel counts that are not
+    multiples of 64, groups, both layouts, all three dtypes, with and without z / bias."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        G = int(rng.choice([1, 1, 2, 3]))
+        D = G * int(rng.integers(1, 100))
+        cases.append((int(rng.integers(1, 4)), int(rng.integers(1, 400)), D,
+                      int(rng.choice([1, 2, 3, 7, 16, 17, 31, 33, 64])),
+                      [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))],
+                      G, bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+                      ["view", "contiguous"][int(rng.integers(0, 2))]))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(12), ids=lambda c: "-".join(map(str, c)).replace("torch.", ""))
+def test_random_shapes_forward_and_backward(case):
+    B, L, D, N, dtype, G, z, bias, layout = case
+    inp = gen(B, L, D, N, dtype, seed=7 * L + D, G=G, z=z, bias=bias)
+    out_ref, ls_ref = ref_fwd(inp)
+    args, kw = call(inp, layout, DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw)
+    assert_out_close(out, out_ref, dtype, dstate=N)
+    assert_state_close(ls, ls_ref)
+    _grads_vs_ref(inp, layout=layout)
