@@ -1,6 +1,7 @@
 """GPU parity of the Mamba-2 SSD forward (s6scan.ssd_combined) against the CPU restatement of
 the reference's chunked pipeline (oracle/ssd_ref.py, pinned by its float64 brute force),
 computed in float64 on the same (16-bit-rounded) inputs."""
+import numpy as np
 import pytest
 import torch
 
@@ -219,3 +220,44 @@ def test_ssd_varlen_states_argument_rules():
                                          return_varlen_states=True, **kw)
     with pytest.raises(AssertionError, match="not supported in backward"):
         out.sum().backward()
+
+
+def _random_ssd_cases(n, seed=4242):
+    """Seeded random problems over the supported space, forward and backward."""
+    rng = np.random.default_rng(seed)
+    flags = ["D", "D_hdim", "z", "bias", "init", "seq", "limit", "final"]
+    cases = []
+    for _ in range(n):
+        G = int(rng.choice([1, 2]))
+        H = G * int(rng.integers(1, 4))
+        opts = tuple(f for f in flags if rng.random() < 0.4)
+        if "D" in opts and "D_hdim" in opts:
+            opts = tuple(f for f in opts if f != "D")
+        cases.append((int(rng.integers(1, 3)), int(rng.integers(1, 600)), H,
+                      int(rng.choice([32, 64, 128])), G, int(rng.choice([32, 64, 128, 256])),
+                      int(rng.choice([64, 128, 256])), opts,
+                      [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_ssd_cases(8), ids=lambda c: "-".join(map(str, c)).replace("torch.", ""))
+def test_ssd_random_problems_forward_and_backward(case):
+    batch, L, H, P, G, N, Q, opts, dtype = case
+    t, kw = make(batch, L, H, P, G, N, dtype, seed=L * 3 + N, opts=opts)
+    final = "final" in opts
+    g = torch.Generator().manual_seed(L + 1)
+    dy = torch.randn(batch, L, H, P, generator=g)
+    dfin = torch.randn(batch, H, P, N, generator=g)
+    names = [k for k, v in t.items() if v.is_floating_point()]
+    gpu = {k: (v.to(DEV).requires_grad_(True) if k in names else v.to(DEV)) for k, v in t.items()}
+    res = mamba_chunk_scan_combined(**gpu, chunk_size=Q, return_final_states=final, **kw)
+    out, fin = res if final else (res, None)
+    cpu = {k: (v.double().requires_grad_(True) if k in names else v) for k, v in t.items()}
+    ref, _, ref_fin = ssd_chunked_ref(**cpu, chunk_size=Q, compute_dtype=torch.float64, **kw)
+    check(out, ref.detach(), dtype, "out")
+    loss = (out.float() * dy.to(DEV)).sum() + ((fin * dfin.to(DEV)).sum() if final else 0.0)
+    loss.backward()
+    rloss = (ref * dy.double()).sum() + ((ref_fin * dfin.double()).sum() if final else 0.0)
+    rloss.backward()
+    for k in names:
+        check_grad(gpu[k].grad, cpu[k].grad, dtype, "d" + k)
