@@ -20,10 +20,14 @@
  *   B, C, dB, dC                                   : [batch, ngroups, dstate, seqlen], any strides
  *   D, delta_bias, dD, ddelta_bias                 : [dim] fp32, any stride
  *   x_ckpt                                         : [batch, s6_num_checkpoints(), dim, dstate]
- *                                                    fp32, contiguous; entry k is the state
- *                                                    after step min((k+1)*S6_CKPT_INTERVAL,
+ *                                                    fp32, contiguous unless x_ckpt_stride
+ *                                                    says otherwise (element strides of the
+ *                                                    four axes, the dstate one 1; all zero =
+ *                                                    contiguous); entry k is the state after
+ *                                                    step min((k+1)*S6_CKPT_INTERVAL,
  *                                                    seqlen)-1, so x_ckpt[:, -1] is the final
- *                                                    state.  It plays the role of the
+ *                                                    state.  s6_bwd never reads that last
+ *                                                    entry.  It plays the role of the
  *                                                    reference kernel's saved `x`
  *                                                    (selective_scan_interface.py:42-47).
  *   last_state                                     : [batch, dim, dstate] fp32 contiguous
@@ -49,7 +53,7 @@
 extern "C" {
 #endif
 
-#define S6_ABI_VERSION 5
+#define S6_ABI_VERSION 6
 #define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
 #define S6_MAX_DSTATE_BWD 64
@@ -86,6 +90,8 @@ typedef struct S6FwdArgs {
   void* out;                int64_t out_stride[3];    /* y + D*u (before the z gate)     */
   void* out_z;              int64_t out_z_stride[3];  /* out * silu(z); has_z only       */
   float* x_ckpt;            /* may be NULL (no backward will follow)                    */
+  int64_t x_ckpt_stride[4]; /* [batch, checkpoint, dim, dstate]: [3] == 1, or all zero =
+                             * contiguous                                                 */
   float* last_state;        /* may be NULL                                               */
   void* workspace;          size_t workspace_bytes;
   /* Optional hipEvent_t pair (NULL = off), recorded on the call's stream right before and
@@ -107,6 +113,7 @@ typedef struct S6BwdArgs {
   const int32_t* cu_seqlens;
   const void* dout;         int64_t dout_stride[3];
   const float* x_ckpt;      /* as written by s6_fwd for the same inputs                  */
+  int64_t x_ckpt_stride[4]; /* as passed to s6_fwd                                       */
   const void* out;          int64_t out_stride[3];    /* pre-gate output; has_z only    */
   void* du;                 int64_t du_stride[3];
   void* ddelta;             int64_t ddelta_stride[3];

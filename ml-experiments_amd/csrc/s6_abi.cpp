@@ -135,6 +135,18 @@ int check_span(const int64_t* s, int es, int64_t Lc, const char* name) {
   return S6_OK;
 }
 
+// x_ckpt strides: all zero (contiguous), or non-negative with the states of a channel
+// contiguous (the kernels load and store a channel's states as one run).
+int check_ckpt(const int64_t* s) {
+  if (s[0] == 0 && s[1] == 0 && s[2] == 0 && s[3] == 0) return S6_OK;
+  for (int i = 0; i < 4; ++i)
+    if (s[i] < 0) return fail(S6_E_INVALID, "x_ckpt has a negative stride");
+  if (s[3] != 1)
+    return fail(S6_E_UNSUPPORTED, "x_ckpt: the dstate stride must be 1, got %lld",
+                (long long)s[3]);
+  return S6_OK;
+}
+
 int check_ptr(const void* p, const char* name) {
   if (p == nullptr) return fail(S6_E_INVALID, "%s must not be NULL", name);
   return S6_OK;
@@ -169,6 +181,16 @@ int check_common(const S6Problem& p, const void* u, const int64_t* su, const voi
   return S6_OK;
 }
 
+// Batch, checkpoint and dim element strides of x_ckpt ([batch, checkpoint, dim, dstate], the
+// dstate stride being 1); all zero = contiguous.
+void ckpt_strides(const int64_t* given, const S6Problem& p, int64_t nck, int64_t* out) {
+  if (given[0] == 0 && given[1] == 0 && given[2] == 0 && given[3] == 0) {
+    out[0] = nck * p.dim * p.dstate; out[1] = p.dim * p.dstate; out[2] = p.dstate;
+  } else {
+    for (int i = 0; i < 3; ++i) out[i] = given[i];
+  }
+}
+
 s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   s6::FwdK k{};
   const S6Problem& p = a.p;
@@ -201,6 +223,7 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   k.cu = a.cu_seqlens; k.nseq = p.nseq;
   k.out = a.out; k.out_z = a.out_z;
   k.x_ckpt = a.x_ckpt; k.nck = pl.nck; k.last_state = a.last_state;
+  ckpt_strides(a.x_ckpt_stride, p, pl.nck, k.sck);
   k.ws_h = pl.K > 1 ? (float*)(ws + pl.off_h) : nullptr;
   k.ws_s = pl.K > 1 ? (float*)(ws + pl.off_s) : nullptr;
   k.ws_r = (pl.K > 1 && p.nseq > 0) ? (int32_t*)(ws + pl.off_r) : nullptr;
@@ -794,6 +817,7 @@ int s6_validate_fwd(const S6FwdArgs* a) {
   if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 3, "out"))) return r;
   if (p.has_z && ((r = check_ptr(a->out_z, "out_z")) || (r = check_strides(a->out_z_stride, 3, "out_z"))))
     return r;
+  if (a->x_ckpt != nullptr && (r = check_ckpt(a->x_ckpt_stride))) return r;
   const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
   const int es = esize(p.io_dtype);
   if ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
@@ -817,7 +841,8 @@ int s6_validate_bwd(const S6BwdArgs* a) {
     return fail(S6_E_UNSUPPORTED, "backward supports dstate <= %d, got %lld", S6_MAX_DSTATE_BWD,
                 (long long)p.dstate);
   if ((r = check_ptr(a->dout, "dout")) || (r = check_strides(a->dout_stride, 3, "dout")) ||
-      (r = check_ptr(a->x_ckpt, "x_ckpt")) || (r = check_ptr(a->du, "du")) ||
+      (r = check_ptr(a->x_ckpt, "x_ckpt")) || (r = check_ckpt(a->x_ckpt_stride)) ||
+      (r = check_ptr(a->du, "du")) ||
       (r = check_strides(a->du_stride, 3, "du")) || (r = check_ptr(a->ddelta, "ddelta")) ||
       (r = check_strides(a->ddelta_stride, 3, "ddelta")) || (r = check_ptr(a->dA, "dA")) ||
       (r = check_strides(a->dA_stride, 2, "dA")) || (r = check_ptr(a->dB, "dB")) ||
@@ -920,6 +945,7 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.A = a->A; k.Dp = a->D; k.bias = a->delta_bias;
     k.cu = a->cu_seqlens; k.nseq = p.nseq;
     k.x_ckpt = a->x_ckpt; k.nck = pl.nck;
+    ckpt_strides(a->x_ckpt_stride, p, pl.nck, k.sck);
     k.du = a->du; k.ddelta = a->ddelta; k.dz = a->dz;
     k.out_z = p.has_z ? a->out_z : nullptr;
     k.dA = a->dA; k.dD = a->dD; k.dbias = a->ddelta_bias; k.dB = a->dB; k.dC = a->dC;

@@ -224,8 +224,8 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const uint32_t Bst = (uint32_t)(p.sB[3] * EB), Cst = (uint32_t)(p.sC[3] * EB);
   float* const pBrow = p.ws_pB + ((b * p.G + g) * p.nJ + j) * p.L * p.NPr + s0;
   float* const pCrow = p.ws_pC + ((b * p.G + g) * p.nJ + j) * p.L * p.NPr + s0;
-  const float* const xck = p.x_ckpt + (b * p.nck * p.D + d) * p.N + s0;  // [b, k, d, s0:]
-  const int64_t xck_step = p.D * p.N;
+  const float* const xck = p.x_ckpt + b * p.sck[0] + d * p.sck[2] + s0;  // [b, k, d, s0:]
+  const int64_t xck_step = p.sck[1];
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.

@@ -256,7 +256,8 @@ struct FwdK {
   const void* Bm; const void* Cm;
   const int32_t* cu; int32_t nseq;
   void* out; void* out_z;
-  float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N]
+  float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N]: states contiguous, element strides
+  int64_t sck[3];               // of the batch, checkpoint and dim axes
   float* last_state;
   float* ws_h;    // [Bsz*D, K, N]  chunk summaries, then carried-in states
   float* ws_s;    // [Bsz*D, K]     sum of Delta since the last sequence start in the chunk

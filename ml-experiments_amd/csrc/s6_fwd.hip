@@ -66,8 +66,8 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
   const float Dv = (FULL && p.has_D) ? p.Dp[d * p.sD] : 0.f;
   // checkpoints: [batch, nck, dim, dstate]
-  float* const xck = (FULL && p.x_ckpt != nullptr) ? p.x_ckpt + (b * p.nck * p.D + d) * p.N : nullptr;
-  const int64_t xck_step = p.D * p.N;
+  float* const xck = (FULL && p.x_ckpt != nullptr) ? p.x_ckpt + b * p.sck[0] + d * p.sck[2] : nullptr;
+  const int64_t xck_step = p.sck[1];
 
   // Buffer resources based at (b, d0, t0) of each [batch, dim, seqlen] tensor.
   const auto rs_u = make_rsrc((const char*)p.u + (b * p.su[0] + d0 * p.su[1] + (int64_t)t0 * p.su[2]) * ES);

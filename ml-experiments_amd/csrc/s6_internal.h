@@ -62,6 +62,7 @@ struct BwdK {
   const void* Bm; const void* Cm;
   const int32_t* cu; int32_t nseq;
   const float* x_ckpt; int64_t nck;   // [Bsz, nck, D, N], as written by the forward
+  int64_t sck[3];                     // its batch, checkpoint and dim strides
   void* du; void* ddelta; void* dz;
   void* out_z; int64_t soz[3];   // out * silu(z) (recompute_out_z), NULL: not written
   float* dA; float* dD; float* dbias; float* dB; float* dC;

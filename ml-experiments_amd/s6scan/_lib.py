@@ -15,7 +15,7 @@ import os
 
 import torch  # noqa: F401  (see module docstring: must precede the HIP library)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 64
@@ -57,7 +57,7 @@ class S6FwdArgs(ctypes.Structure):
         ("cu_seqlens", _vp),
         ("out", _vp), ("out_stride", _a(3)),
         ("out_z", _vp), ("out_z_stride", _a(3)),
-        ("x_ckpt", _vp),
+        ("x_ckpt", _vp), ("x_ckpt_stride", _a(4)),
         ("last_state", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("kernel_events", _vp * 2),
@@ -77,7 +77,7 @@ class S6BwdArgs(ctypes.Structure):
         ("delta_bias", _vp), ("delta_bias_stride", _i64),
         ("cu_seqlens", _vp),
         ("dout", _vp), ("dout_stride", _a(3)),
-        ("x_ckpt", _vp),
+        ("x_ckpt", _vp), ("x_ckpt_stride", _a(4)),
         ("out", _vp), ("out_stride", _a(3)),
         ("du", _vp), ("du_stride", _a(3)),
         ("ddelta", _vp), ("ddelta_stride", _a(3)),

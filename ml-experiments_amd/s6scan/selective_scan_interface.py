@@ -152,11 +152,28 @@ def _events(kernel_events):
     return tuple(ctypes.c_void_p(e.cuda_event) for e in kernel_events)
 
 
+def _ckpt_check(x_ckpt, batch, nck, dim, dstate, device):
+    want = (batch, nck, dim, dstate)
+    if (tuple(x_ckpt.shape) != want or x_ckpt.dtype != torch.float32
+            or x_ckpt.device != device or (dstate > 1 and x_ckpt.stride(3) != 1)):
+        raise ValueError(f"x_ckpt must be a float32 view of shape {want} on {device} "
+                         "with unit dstate stride")
+    return x_ckpt
+
+
+def _ckpt_strides(x_ckpt):
+    # the dstate axis is contiguous (a size-1 axis may carry any stride in torch)
+    return (0,) * 4 if x_ckpt is None else tuple(x_ckpt.stride()[:3]) + (1,)
+
+
 def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
                            delta_softplus=False, cu_seqlens=None, want_ckpt=True,
-                           want_last_state=False, kernel_events=None):
+                           want_last_state=False, kernel_events=None, x_ckpt_out=None):
     """One forward launch.  Returns (out, out_z, x_ckpt, last_state); out_z is None without
     z, x_ckpt is None unless ``want_ckpt``, last_state is None unless ``want_last_state``.
+    ``x_ckpt_out``: optional preallocated checkpoint view [batch, nck, dim, dstate] fp32 with
+    a unit dstate stride and any other strides (nck = ceil(seqlen / 8)), written in place of
+    a new contiguous one.
     ``kernel_events``: optional pair of already-recorded torch.cuda.Events that the library
     re-records around its main scan kernel (measurement only)."""
     dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
@@ -167,8 +184,11 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         out = torch.empty_like(u)
         out_z = torch.empty_like(u) if z is not None else None
         nck = _lib.LIB.s6_num_checkpoints(ctypes.byref(prob))
-        x_ckpt = (torch.empty(batch, nck, dim, dstate, dtype=torch.float32, device=u.device)
-                  if want_ckpt else None)
+        if x_ckpt_out is not None:
+            x_ckpt = _ckpt_check(x_ckpt_out, batch, nck, dim, dstate, u.device)
+        else:
+            x_ckpt = (torch.empty(batch, nck, dim, dstate, dtype=torch.float32, device=u.device)
+                      if want_ckpt else None)
         nls = nseq if nseq > 0 else batch
         last_state = (torch.empty(nls, dim, dstate, dtype=torch.float32, device=u.device)
                       if want_last_state else None)
@@ -186,7 +206,7 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         args.cu_seqlens = _ptr(cu_seqlens)
         args.out, args.out_stride = _ptr(out), _strides(out, 3)
         args.out_z, args.out_z_stride = _ptr(out_z), _strides(out_z, 3)
-        args.x_ckpt = _ptr(x_ckpt)
+        args.x_ckpt, args.x_ckpt_stride = _ptr(x_ckpt), _ckpt_strides(x_ckpt)
         args.last_state = _ptr(last_state)
         nbytes = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=u.device)
@@ -243,7 +263,9 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
         args.delta_bias_stride = delta_bias.stride(0) if delta_bias is not None else 0
         args.cu_seqlens = _ptr(cu_seqlens)
         args.dout, args.dout_stride = _ptr(dout), _strides(dout, 3)
-        args.x_ckpt = _ptr(x_ckpt)
+        nck = _lib.LIB.s6_num_checkpoints(ctypes.byref(prob))
+        _ckpt_check(x_ckpt, batch, nck, dim, dstate, u.device)
+        args.x_ckpt, args.x_ckpt_stride = _ptr(x_ckpt), _ckpt_strides(x_ckpt)
         args.out, args.out_stride = _ptr(out), _strides(out, 3)
         args.du, args.du_stride = _ptr(du), _strides(du, 3)
         args.ddelta, args.ddelta_stride = _ptr(ddelta), _strides(ddelta, 3)

@@ -123,6 +123,29 @@ def test_validate_fwd_ok_and_errors():
     assert "cu_seqlens" in _lib.last_error()
 
 
+def test_validate_checkpoint_strides():
+    # x_ckpt strides [batch, checkpoint, dim, dstate]: all zero = contiguous; any non-negative
+    # batch / checkpoint / dim strides with a unit dstate stride (the native-module layout,
+    # [batch, nck, dim, 2*dstate] storage with the states in the first half, among them);
+    # negative strides and strided states are rejected
+    a = fwd_args()
+    a.x_ckpt = 0x10000
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.OK
+    nck = _lib.LIB.s6_num_checkpoints(ctypes.byref(a.p))
+    N, D = a.p.dstate, a.p.dim
+    a.x_ckpt_stride = (nck * D * 2 * N, D * 2 * N, 2 * N, 1)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.OK
+    a.x_ckpt_stride = (0, 0, -N, 1)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
+    assert "x_ckpt has a negative stride" in _lib.last_error()
+    a.x_ckpt_stride = (nck * D * 2 * N, D * 2 * N, 2 * N, 2)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_UNSUPPORTED
+    assert "dstate stride must be 1" in _lib.last_error()
+    a.x_ckpt = None  # no checkpoints written: strides are not looked at
+    a.x_ckpt_stride = (0, 0, -1, 0)
+    assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.OK
+
+
 def test_validate_bwd_dstate_limits():
     def args(N):
         a = _lib.S6BwdArgs()

@@ -343,3 +343,52 @@ def test_random_shapes_forward_and_backward(case):
     assert_out_close(out, out_ref, dtype, dstate=N)
     assert_state_close(ls, ls_ref)
     _grads_vs_ref(inp, layout=layout)
+
+
+@pytest.mark.parametrize("z,bias,layout", [(False, False, "view"), (True, True, "view"),
+                                           (True, False, "contiguous")])
+def test_native_module_contract(z, bias, layout):
+    """s6scan.selective_scan_cuda against the drop-in op, called the way the reference's
+    Python calls its native module: fwd with 4-D B/C, last_state read as x[:, :, -1, 1::2],
+    bwd with the saved x and out, a preallocated dz, and recompute_out_z."""
+    from s6scan import selective_scan_cuda as ssc
+    inp = gen(2, 203, 96, 16, torch.bfloat16, seed=41, G=2, z=z, bias=bias)
+    args, kw = call(inp, layout, DEV)
+    u, delta, A, B, C = args
+    B4, C4 = (B.unsqueeze(1), C.unsqueeze(1)) if B.dim() == 3 else (B, C)
+    Dv, zz, db, sp = kw["D"], kw["z"], kw["delta_bias"], kw["delta_softplus"]
+    res = ssc.fwd(u, delta, A, B4, C4, Dv, zz, db, sp)
+    out, x = res[0], res[1]
+    assert len(res) == (3 if z else 2)
+    assert x.shape == (2, 96, -(-203 // 8), 32) and x.dtype == torch.float32
+    want_out, want_ls = s6scan.selective_scan_fn(*args, **kw)
+    got_out = res[2] if z else out
+    assert torch.equal(got_out, want_out)
+    assert torch.equal(x[:, :, -1, 1::2], want_ls)
+    # backward: the same gradients as the drop-in op's autograd
+    dy = views(inp["dy"].to(DEV), layout)
+    leaves = [t.detach().clone().requires_grad_(True) if t is not None else None
+              for t in (u, delta, A, B, C, Dv, zz, db)]
+    o = s6scan.selective_scan_fn(*leaves[:5], D=leaves[5], z=leaves[6], delta_bias=leaves[7],
+                                 delta_softplus=sp)
+    o.backward(dy)
+    dz_pre = torch.empty_like(zz) if z else None
+    g = ssc.bwd(u, delta, A, B4, C4, Dv, zz, db, dy, x, out if z else None, dz_pre, sp, z)
+    assert len(g) == (9 if z else 7)
+    names = ["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias"]
+    wants = [leaves[0].grad, leaves[1].grad, leaves[2].grad, leaves[3].grad, leaves[4].grad,
+             leaves[5].grad, leaves[7].grad if bias else None]
+    for name, got, want in zip(names, g[:7], wants):
+        if want is None:
+            continue
+        if name in ("dB", "dC"):
+            assert got.dtype == torch.float32 and got.dim() == 4  # as the reference kernel's
+            got = got.squeeze(1) if want.dim() == 3 else got
+        # autograd stores a leaf's gradient in the leaf's dtype
+        assert torch.equal(got.to(want.dtype), want), name
+    if z:
+        assert g[7] is dz_pre and torch.equal(dz_pre, leaves[6].grad)
+        # recompute_out_z is out * silu(z) from the saved (rounded) out, as the reference's
+        zf = zz.float()
+        ref_oz = out.float() * zf * torch.sigmoid(zf)
+        assert torch.allclose(g[8].float(), ref_oz, rtol=1e-2, atol=1e-3 * ref_oz.abs().max().item())
