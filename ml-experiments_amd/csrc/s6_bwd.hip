@@ -227,6 +227,16 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const float* const xck = p.x_ckpt + b * p.sck[0] + d * p.sck[2] + s0;  // [b, k, d, s0:]
   const int64_t xck_step = p.sck[1];
 
+  // LDS_A: exp(Delta A) of the current segment and half is written by the forward recompute
+  // and read back by the reverse sweep, one step ahead, from [step][4-state quarter][lane]
+  // (each lane touches only its own entries: no barrier; 16 KB per wave).  Without it the
+  // reverse sweep recomputes the exponentials.  The z-gated and softplus kernels recompute:
+  // they are at their VGPR limit, and the 8 registers of the read-ahead spill (z-gated block
+  // kernel measured 17% slower with it).
+  constexpr bool LDS_A = !HAS_Z && DTM != kDtSoftplus;
+  static_assert(HS == 8, "two float4 per step");
+  __shared__ float4 sa[LDS_A ? SEG * 2 * kWave : 1];
+
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.
   float un[SEG], dn[SEG], on[SEG], zn[SEG], yn[SEG], hn[NS];
@@ -308,21 +318,40 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
             const float dtu = dt[i] * uu[i];
             auto body = [&](auto st_tag) {  // ST: a sequence starts at this step, h_{t-1} = 0
               constexpr bool ST = decltype(st_tag)::value;
+              float av[HS];
 #pragma unroll
               for (int k = 0; k < HS; ++k) {
                 const float b_ = dtu * bcur.get(k);
-                h[k] = ST ? b_ : fmaf(fast_exp2(dt[i] * Ap[hh * HS + k]), h[k], b_);
+                av[k] = ST ? 0.f : fast_exp2(dt[i] * Ap[hh * HS + k]);
+                h[k] = ST ? b_ : fmaf(av[k], h[k], b_);
                 hs[i][k] = h[k];
+              }
+              if (LDS_A && !ST) {
+                sa[(i * 2) * kWave + lane] = make_float4(av[0], av[1], av[2], av[3]);
+                sa[(i * 2 + 1) * kWave + lane] = make_float4(av[4], av[5], av[6], av[7]);
               }
             };
             if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
           }
         }
       }
-      // Reverse sweep.
+      // Reverse sweep.  With LDS_A, exp(Delta A) comes back from LDS one step ahead of its use.
+      float4 an_lo{}, an_hi{};
+      if (LDS_A) {
+        an_lo = sa[((SEG - 1) * 2) * kWave + lane];
+        an_hi = sa[((SEG - 1) * 2 + 1) * kWave + lane];
+      }
 #pragma unroll
       for (int i = SEG - 1; i >= 0; --i) {
         const int t = ts + i;
+        // exp(Delta A) of this step as the recompute stored it (garbage at a sequence start or
+        // past the input's end, where it is not used); the next step's read goes out now,
+        // whether or not this step is inside the input, so step i always gets entry i.
+        const float av[HS] = {an_lo.x, an_lo.y, an_lo.z, an_lo.w, an_hi.x, an_hi.y, an_hi.z, an_hi.w};
+        if (LDS_A && i > 0) {
+          an_lo = sa[((i - 1) * 2) * kWave + lane];
+          an_hi = sa[((i - 1) * 2 + 1) * kWave + lane];
+        }
         if (t < te) {
           bnx.touch();
           cnx.touch();
@@ -335,10 +364,10 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
           } else if (s > 0) {  // first half of the previous segment
             bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - SEG - t0) * Bst));
           }
-          // Delta passes through an empty asm so that exp(Delta A) is recomputed here rather
-          // than kept live from the recompute above (64 more VGPRs per lane).
+          // Without LDS_A, Delta passes through an empty asm so that exp(Delta A) is recomputed
+          // here rather than kept live from the recompute above (64 more VGPRs per lane).
           float dti = dt[i];
-          asm volatile("" : "+v"(dti));
+          if (!LDS_A) asm volatile("" : "+v"(dti));
           const float dtu = dti * uu[i];
           float pB[HS], pC[HS];
           auto body = [&](auto st_tag) {  // ST: a sequence starts at this step
@@ -348,12 +377,15 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
               const int n = hh * HS + k;
               const float lam = fmaf(ccur.get(k), dy[i], gs[n]);
               if (!ST) {
-                const float a = fast_exp2(dti * Ap[n]);
                 const float hp = (i > 0) ? hs[i - 1][k] : hst[n];
-                const float q = lam * (a * hp);
+                const float a = LDS_A ? av[k] : fast_exp2(dti * Ap[n]);
+                const float gl = a * lam;      // g_t = abar_t lambda_t
+                // q_t = g_t h_{t-1}; the recompute path keeps the product order its register
+                // allocation was measured with
+                const float q = LDS_A ? gl * hp : lam * (a * hp);
                 dAacc[n] = fmaf(q, dti, dAacc[n]);
                 s2[i] = fmaf(q, Ap[n], s2[i]);
-                gs[n] = a * lam;
+                gs[n] = gl;
               } else {
                 gs[n] = 0.f;
               }
