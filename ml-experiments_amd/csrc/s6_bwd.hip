@@ -227,15 +227,17 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const float* const xck = p.x_ckpt + b * p.sck[0] + d * p.sck[2] + s0;  // [b, k, d, s0:]
   const int64_t xck_step = p.sck[1];
 
-  // LDS_A: exp(Delta A) of the current segment and half is written by the forward recompute
-  // and read back by the reverse sweep, one step ahead, from [step][4-state quarter][lane]
-  // (each lane touches only its own entries: no barrier; 16 KB per wave).  Without it the
-  // reverse sweep recomputes the exponentials.  The z-gated and softplus kernels recompute:
-  // they are at their VGPR limit, and the 8 registers of the read-ahead spill (z-gated block
-  // kernel measured 17% slower with it).
+  // The forward recompute of a segment's half hands the reverse sweep one [step][8] row per
+  // step through LDS, [step][4-state quarter][lane] (each lane touches only its own entries:
+  // no barrier; 16 KB per wave), read back ahead of use:
+  //   LDS_A: exp(Delta A), which the reverse sweep then need not recompute;
+  //   LDS_H (z-gated and softplus kernels): the recomputed states themselves, which frees the
+  //   64 VGPRs that hold them otherwise; these kernels are at their VGPR limit (256) and
+  //   recompute exp(Delta A) instead.
   constexpr bool LDS_A = !HAS_Z && DTM != kDtSoftplus;
+  constexpr bool LDS_H = !LDS_A;
   static_assert(HS == 8, "two float4 per step");
-  __shared__ float4 sa[LDS_A ? SEG * 2 * kWave : 1];
+  __shared__ float4 sa[SEG * 2 * kWave];
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.
@@ -330,27 +332,43 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
                 sa[(i * 2) * kWave + lane] = make_float4(av[0], av[1], av[2], av[3]);
                 sa[(i * 2 + 1) * kWave + lane] = make_float4(av[4], av[5], av[6], av[7]);
               }
+              if (LDS_H) {
+                sa[(i * 2) * kWave + lane] = make_float4(h[0], h[1], h[2], h[3]);
+                sa[(i * 2 + 1) * kWave + lane] = make_float4(h[4], h[5], h[6], h[7]);
+              }
             };
             if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
           }
         }
       }
-      // Reverse sweep.  With LDS_A, exp(Delta A) comes back from LDS one step ahead of its use.
-      float4 an_lo{}, an_hi{};
-      if (LDS_A) {
-        an_lo = sa[((SEG - 1) * 2) * kWave + lane];
-        an_hi = sa[((SEG - 1) * 2 + 1) * kWave + lane];
+      // Reverse sweep.  The LDS rows come back ahead of their use: row i - 1 (LDS_A) or
+      // row i - 2 (LDS_H, which also needs row i - 1 at step i).
+      float4 c_lo{}, c_hi{}, p_lo{}, p_hi{};  // rows of steps i and (LDS_H) i - 1
+      c_lo = sa[((SEG - 1) * 2) * kWave + lane];
+      c_hi = sa[((SEG - 1) * 2 + 1) * kWave + lane];
+      if (LDS_H) {
+        p_lo = sa[((SEG - 2) * 2) * kWave + lane];
+        p_hi = sa[((SEG - 2) * 2 + 1) * kWave + lane];
       }
 #pragma unroll
       for (int i = SEG - 1; i >= 0; --i) {
         const int t = ts + i;
-        // exp(Delta A) of this step as the recompute stored it (garbage at a sequence start or
-        // past the input's end, where it is not used); the next step's read goes out now,
-        // whether or not this step is inside the input, so step i always gets entry i.
-        const float av[HS] = {an_lo.x, an_lo.y, an_lo.z, an_lo.w, an_hi.x, an_hi.y, an_hi.z, an_hi.w};
+        // Step i's rows as the recompute stored them (garbage at a sequence start or past the
+        // input's end, where they are not used); the next read goes out now, whether or not
+        // this step is inside the input, so step i always gets row i.
+        const float rc[HS] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
+        const float rp[HS] = {p_lo.x, p_lo.y, p_lo.z, p_lo.w, p_hi.x, p_hi.y, p_hi.z, p_hi.w};
         if (LDS_A && i > 0) {
-          an_lo = sa[((i - 1) * 2) * kWave + lane];
-          an_hi = sa[((i - 1) * 2 + 1) * kWave + lane];
+          c_lo = sa[((i - 1) * 2) * kWave + lane];
+          c_hi = sa[((i - 1) * 2 + 1) * kWave + lane];
+        }
+        if (LDS_H) {
+          c_lo = p_lo;
+          c_hi = p_hi;
+          if (i > 1) {
+            p_lo = sa[((i - 2) * 2) * kWave + lane];
+            p_hi = sa[((i - 2) * 2 + 1) * kWave + lane];
+          }
         }
         if (t < te) {
           bnx.touch();
@@ -377,8 +395,8 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
               const int n = hh * HS + k;
               const float lam = fmaf(ccur.get(k), dy[i], gs[n]);
               if (!ST) {
-                const float hp = (i > 0) ? hs[i - 1][k] : hst[n];
-                const float a = LDS_A ? av[k] : fast_exp2(dti * Ap[n]);
+                const float hp = (i > 0) ? (LDS_H ? rp[k] : hs[i - 1][k]) : hst[n];
+                const float a = LDS_A ? rc[k] : fast_exp2(dti * Ap[n]);
                 const float gl = a * lam;      // g_t = abar_t lambda_t
                 // q_t = g_t h_{t-1}; the recompute path keeps the product order its register
                 // allocation was measured with
@@ -391,7 +409,7 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
               }
               s1[i] = fmaf(lam, bcur.get(k), s1[i]);
               pB[k] = lam * dtu;
-              pC[k] = dy[i] * hs[i][k];
+              pC[k] = dy[i] * (LDS_H ? rc[k] : hs[i][k]);
             }
           };
           if ((smask >> i) & 1u) body(std::true_type{}); else body(std::false_type{});
