@@ -231,13 +231,14 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   // step through LDS, [step][4-state quarter][lane] (each lane touches only its own entries:
   // no barrier; 16 KB per wave), read back ahead of use:
   //   LDS_A: exp(Delta A), which the reverse sweep then need not recompute;
-  //   LDS_H (z-gated and softplus kernels): the recomputed states themselves, which frees the
-  //   64 VGPRs that hold them otherwise; these kernels are at their VGPR limit (256) and
-  //   recompute exp(Delta A) instead.
+  //   LDS_H (z-gated kernels): the recomputed states themselves, which frees the 64 VGPRs that
+  //   hold them otherwise.  These kernels are at their VGPR limit (256) and recompute
+  //   exp(Delta A); without LDS_H they spill, which the out_z recompute pays for.
+  // The softplus kernel without z uses neither: both measured slower there.
   constexpr bool LDS_A = !HAS_Z && DTM != kDtSoftplus;
-  constexpr bool LDS_H = !LDS_A;
+  constexpr bool LDS_H = HAS_Z;
   static_assert(HS == 8, "two float4 per step");
-  __shared__ float4 sa[SEG * 2 * kWave];
+  __shared__ float4 sa[(LDS_A || LDS_H) ? SEG * 2 * kWave : 1];
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.
@@ -328,11 +329,11 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
                 h[k] = ST ? b_ : fmaf(av[k], h[k], b_);
                 hs[i][k] = h[k];
               }
-              if (LDS_A && !ST) {
+              if constexpr (LDS_A && !ST) {
                 sa[(i * 2) * kWave + lane] = make_float4(av[0], av[1], av[2], av[3]);
                 sa[(i * 2 + 1) * kWave + lane] = make_float4(av[4], av[5], av[6], av[7]);
               }
-              if (LDS_H) {
+              if constexpr (LDS_H) {
                 sa[(i * 2) * kWave + lane] = make_float4(h[0], h[1], h[2], h[3]);
                 sa[(i * 2 + 1) * kWave + lane] = make_float4(h[4], h[5], h[6], h[7]);
               }
@@ -344,9 +345,11 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
       // Reverse sweep.  The LDS rows come back ahead of their use: row i - 1 (LDS_A) or
       // row i - 2 (LDS_H, which also needs row i - 1 at step i).
       float4 c_lo{}, c_hi{}, p_lo{}, p_hi{};  // rows of steps i and (LDS_H) i - 1
-      c_lo = sa[((SEG - 1) * 2) * kWave + lane];
-      c_hi = sa[((SEG - 1) * 2 + 1) * kWave + lane];
-      if (LDS_H) {
+      if constexpr (LDS_A || LDS_H) {
+        c_lo = sa[((SEG - 1) * 2) * kWave + lane];
+        c_hi = sa[((SEG - 1) * 2 + 1) * kWave + lane];
+      }
+      if constexpr (LDS_H) {
         p_lo = sa[((SEG - 2) * 2) * kWave + lane];
         p_hi = sa[((SEG - 2) * 2 + 1) * kWave + lane];
       }
@@ -358,11 +361,13 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
         // this step is inside the input, so step i always gets row i.
         const float rc[HS] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
         const float rp[HS] = {p_lo.x, p_lo.y, p_lo.z, p_lo.w, p_hi.x, p_hi.y, p_hi.z, p_hi.w};
-        if (LDS_A && i > 0) {
-          c_lo = sa[((i - 1) * 2) * kWave + lane];
-          c_hi = sa[((i - 1) * 2 + 1) * kWave + lane];
+        if constexpr (LDS_A) {
+          if (i > 0) {
+            c_lo = sa[((i - 1) * 2) * kWave + lane];
+            c_hi = sa[((i - 1) * 2 + 1) * kWave + lane];
+          }
         }
-        if (LDS_H) {
+        if constexpr (LDS_H) {
           c_lo = p_lo;
           c_hi = p_hi;
           if (i > 1) {
