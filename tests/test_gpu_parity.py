@@ -20,8 +20,10 @@ DEV = "cuda"
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "s6_golden.npz")
 
 
-def gen(B, L, D, N, dtype, seed, G=1, z=False, bias=False, shift=-1.0):
-    """Channel-last producer tensors ([B, L, *]) like the workload generator."""
+def gen(B, L, D, N, dtype, seed, G=1, z=False, bias=False, shift=-1.0, softplus=None):
+    """Channel-last producer tensors ([B, L, *]) like the workload generator.  With a bias,
+    delta_softplus is on unless ``softplus=False``; then delta is already positive and the
+    bias is a small positive shift, so delta + bias stays a valid step size."""
     g = torch.Generator("cpu").manual_seed(seed)
     x = torch.randn(B, L, D, generator=g)
     dtr = torch.randn(B, L, D, generator=g)
@@ -31,10 +33,13 @@ def gen(B, L, D, N, dtype, seed, G=1, z=False, bias=False, shift=-1.0):
     Dv = torch.randn(D, generator=g)
     zz = torch.randn(B, L, D, generator=g).to(dtype) if z else None
     bb = 0.3 * torch.randn(D, generator=g) if bias else None
-    dl = (0.5 * dtr + shift) if bias else torch.nn.functional.softplus(0.5 * dtr + shift)
+    sp = bias if softplus is None else softplus
+    dl = (0.5 * dtr + shift) if sp else torch.nn.functional.softplus(0.5 * dtr + shift)
+    if bias and not sp:
+        bb = bb.abs() / 3
     dy = torch.randn(B, L, D, generator=g).to(dtype)
     return dict(x=x.to(dtype), delta=dl.to(dtype), A=A, B=Bm.to(dtype), C=Cm.to(dtype), D=Dv,
-                z=zz, bias=bb, dy=dy, G=G)
+                z=zz, bias=bb, dy=dy, G=G, softplus=sp)
 
 
 def views(t, layout):
@@ -58,7 +63,7 @@ def call(inp, layout, device, cu=None, last=True):
     args = [views(dev(inp["x"]), layout), views(dev(inp["delta"]), layout), dev(inp["A"]),
             bc_views(dev(inp["B"]), inp["G"], layout), bc_views(dev(inp["C"]), inp["G"], layout)]
     kw = dict(D=dev(inp["D"]), z=views(dev(inp["z"]), layout), delta_bias=dev(inp["bias"]),
-              delta_softplus=inp["bias"] is not None, return_last_state=last)
+              delta_softplus=inp.get("softplus", inp["bias"] is not None), return_last_state=last)
     return args, kw
 
 
@@ -220,14 +225,42 @@ def test_backward_matches_autograd_of_restatement(case):
     _grads_vs_ref(inp)
 
 
+@pytest.mark.parametrize("z", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bias_without_softplus(z, dtype):
+    """delta + delta_bias with delta_softplus off (the kernels' bias-only delta mode), with
+    and without the z gate, a partial last segment and several chunks.  The larger steps of
+    this mode make y cancel more: there the fp32 restatement itself is ~1e-6 off the exact
+    value (measured: -0.04081440 vs -0.04081545, while the kernel gives -0.04081542), so
+    fp32 is held to the fp32 bar against the float64 evaluation of the same restatement."""
+    inp = gen(2, 1203, 96, 16, dtype, seed=17, z=z, bias=True, softplus=False)
+    if dtype == torch.float32:
+        rargs, rkw = call(inp, "view", "cpu")
+        r64 = [a.double() if a.is_floating_point() else a for a in rargs]
+        rkw = {k: (v.double() if torch.is_tensor(v) and v.is_floating_point() else v) for k, v in rkw.items()}
+        out_ref, ls_ref = selective_scan_ref(*r64, **rkw, compute_dtype=torch.float64)
+    else:
+        out_ref, ls_ref = ref_fwd(inp)
+    args, kw = call(inp, "view", DEV)
+    assert kw["delta_softplus"] is False and kw["delta_bias"] is not None
+    out, ls = s6scan.selective_scan_fn(*args, **kw)
+    assert_out_close(out, out_ref, dtype, dstate=16)
+    assert_state_close(ls, ls_ref)
+    _grads_vs_ref(inp)
+
+
 def test_backward_contiguous_layout():
     inp = gen(2, 160, 128, 16, torch.bfloat16, seed=9, z=True, bias=True)
     _grads_vs_ref(inp, layout="contiguous")
 
 
+@pytest.mark.parametrize("zb", [True, False], ids=["z_softplus", "plain"])
 @pytest.mark.parametrize("cu", [[0, 100, 101, 450, 700, 1000], [0, 32, 64, 96, 1000], [0, 1000]])
-def test_varlen_forward_and_backward(cu):
-    inp = gen(1, 1000, 64, 16, torch.float32, seed=11, z=True, bias=True)
+def test_varlen_forward_and_backward(cu, zb):
+    """Sequence starts inside segments, on segment boundaries and at single-step sequences,
+    for the z-gated softplus backward and the plain one (they keep different values in LDS
+    between the recompute and the reverse sweep)."""
+    inp = gen(1, 1000, 64, 16, torch.float32, seed=11, z=zb, bias=zb)
     cu = torch.tensor(cu, dtype=torch.int32)
     out_ref, ls_ref = ref_fwd(inp, cu)
     args, kw = call(inp, "view", DEV)
