@@ -46,7 +46,11 @@ __device__ inline void store_state(float* dst, const float (&h)[NS], int N) {
     for (int n = 0; n < NS; n += 4)
       *reinterpret_cast<float4*>(dst + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
   } else {
-    for (int n = 0; n < N; ++n) dst[n] = h[n];
+    // Unrolled over NS with a predicate: a runtime-bounded loop would index h dynamically
+    // and force the whole state array out of registers into scratch.
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      if (n < N) dst[n] = h[n];
   }
 }
 
