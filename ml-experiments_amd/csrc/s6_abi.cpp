@@ -52,11 +52,14 @@ struct Plan {
   int64_t nsg, NPr;  // backward: state groups of 16, partial row width
 };
 
-// States held per lane by the kernels: the forward pads dstate to 8/16/32/64; the backward
-// to 8/16 and, above 16, splits it into groups of 16 (padded to a multiple of 16).  B and C
+// States held per lane by the kernels: the forward pads dstate to 8/16/32 and above 32
+// splits it into groups of 16, one wave per group; the backward pads to 8/16 and above 16
+// splits it into groups of 16 (B / C rows padded to a multiple of 16 states).  B and C
 // rows are read as NS contiguous values, so a row is used in place only when dstate == NS,
 // the state axis is contiguous and 16-bit rows are 4-byte aligned.
-int64_t ns_fwd(int64_t N) { return N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
+int64_t ns_fwd(int64_t N) { return N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : ceil_div(N, 16) * 16; }
+// Forward state groups: above 32 states a workgroup holds one wave per group of 16.
+int64_t nsg_fwd(int64_t N) { return N <= 32 ? 1 : ceil_div(N, 16); }
 int64_t ns_bwd(int64_t N) { return N <= 8 ? 8 : ceil_div(N, s6::kBwdGroup) * s6::kBwdGroup; }
 
 bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_t NS) {
@@ -76,7 +79,9 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   pl.nJ = ceil_div(pl.Dg, 64);
   pl.nDblk = p.ngroups * pl.nJ;
   const int64_t chw = p.batch * pl.nDblk;
-  const int64_t ktarget = ceil_div(bwd ? kTargetWavesBwd : kTargetWavesFwd, chw > 0 ? chw : 1);
+  const int64_t waves_per_chunk = chw * (bwd ? 1 : nsg_fwd(p.dstate));
+  const int64_t ktarget =
+      ceil_div(bwd ? kTargetWavesBwd : kTargetWavesFwd, waves_per_chunk > 0 ? waves_per_chunk : 1);
   int64_t Lc = ceil_div(p.seqlen, ktarget > 0 ? ktarget : 1);
   const int64_t min_chunk = bwd ? kMinChunkBwd : kMinChunkFwd;
   if (Lc < min_chunk) Lc = min_chunk;
@@ -230,6 +235,7 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   k.K = pl.K; k.Lc = pl.Lc;
   k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
   k.nDblk = pl.nDblk;
+  k.nsg = (int32_t)nsg_fwd(p.dstate);
   return k;
 }
 

@@ -265,6 +265,7 @@ struct FwdK {
   int64_t K, Lc;  // number of chunks and chunk length (multiple of kCk)
   int32_t has_D, has_z, has_bias, softplus;
   int64_t nDblk;  // G * ceil(D / G / 64): 64-channel blocks per batch
+  int32_t nsg;    // dstate > 32: groups of 16 states, one wave each per workgroup (<= 4)
 };
 
 }  // namespace s6

@@ -22,8 +22,16 @@ namespace s6 {
 
 // MODE 0: chunk summary; 1: output pass; 2: output pass with the silu(z) gate.
 // DTM: how Delta is formed from the delta input (kDtRaw / kDtBias / kDtSoftplus).
-template <typename Tio, typename Tbc, int NS, int MODE, int DTM>
-__global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
+// MULTI (dstate > 32): the workgroup holds one wave per group of NS = 16 states (p.nsg
+// waves) of the same 64 channels and chunk.  The state groups scan independently; in the
+// output pass each wave's share of y (its states' C h) goes through LDS once per 8-step
+// block, and the waves then split the block's steps to sum the groups in a fixed order, add
+// D u, gate and store.  This keeps every wave at the register footprint of 16 states; at
+// 17-32 states one wave holding them all measured faster (2 groups do not pay for the
+// duplicated per-step work and the barrier).
+template <typename Tio, typename Tbc, int NS, int MODE, int DTM, bool MULTI>
+__global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
+    __attribute__((amdgpu_waves_per_eu(MULTI ? 4 : 1))) fwd_scan(FwdK p) {
   constexpr bool FULL = MODE != 0;
   constexpr bool HAS_Z = MODE == 2;
   constexpr int TB = kCk;  // steps per unrolled block = checkpoint interval
@@ -31,7 +39,14 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   constexpr int EB = Elem<Tbc>::kSize;
   constexpr int GS = NS < kGroupStates<Tbc> ? NS : kGroupStates<Tbc>;  // states per scalar group
   constexpr int NG = NS / GS;
-  const int lane = threadIdx.x;
+  static_assert(!MULTI || NS == 16, "state groups of 16");
+  const int lane = threadIdx.x & (kWave - 1);
+  // State group of this wave, made wave-uniform (an SGPR) so that the B / C row addresses
+  // derived from it stay scalar and their loads stay on the scalar cache.
+  const int gn = MULTI ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)) : 0;
+  const int s0 = gn * NS;                                   // its first state
+  // MULTI output pass: the groups' shares of y, [block parity][group][step][lane].
+  __shared__ float ysh[2][4][TB][kWave];
   const BlockPos bp = block_pos(p.Bsz * p.nDblk);
   const int64_t Dg = p.D / p.G;
   const int64_t nJ = (Dg + kWave - 1) / kWave;
@@ -47,26 +62,27 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const int L = (int)p.L;
   const int t0 = c * (int)p.Lc;
   const int t1 = min(t0 + (int)p.Lc, L);
-  const int N = (int)p.N;
+  const int N = (int)p.N - s0;  // states of the group (may exceed NS)
+  const int Nw = min(N, NS);     // states this wave owns
   const bool varlen = p.nseq > 0;
 
   float Ap[NS];
   float h[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    Ap[n] = (n < N) ? p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e : 0.f;
+    Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
     h[n] = 0.f;
   }
   const int64_t ch = b * p.D + d;  // channel index for workspaces
   if (FULL && c > 0) {
-    const float* hin = p.ws_h + (ch * p.K + c) * p.N;
+    const float* hin = p.ws_h + (ch * p.K + c) * p.N + s0;
 #pragma unroll
     for (int n = 0; n < NS; ++n) h[n] = (n < N) ? hin[n] : 0.f;
   }
   const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
   const float Dv = (FULL && p.has_D) ? p.Dp[d * p.sD] : 0.f;
   // checkpoints: [batch, nck, dim, dstate]
-  float* const xck = (FULL && p.x_ckpt != nullptr) ? p.x_ckpt + b * p.sck[0] + d * p.sck[2] : nullptr;
+  float* const xck = (FULL && p.x_ckpt != nullptr) ? p.x_ckpt + b * p.sck[0] + d * p.sck[2] + s0 : nullptr;
   const int64_t xck_step = p.sck[1];
 
   // Buffer resources based at (b, d0, t0) of each [batch, dim, seqlen] tensor.
@@ -89,8 +105,8 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
   const uint32_t st_z = HAS_Z ? (uint32_t)(p.sz[2] * ES) : 0u;
   const uint32_t st_oz = HAS_Z ? (uint32_t)(p.soz[2] * ES) : 0u;
   // B / C rows of this wave's (batch, group), from step t0; 32-bit byte offsets per step.
-  const char* const Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3]) * EB;
-  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3]) * EB;
+  const char* const Bbase = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1] + (int64_t)t0 * p.sB[3] + s0) * EB;
+  const char* const Cbase = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3] + s0) * EB;
   const uint32_t Bst = (uint32_t)(p.sB[3] * EB), Cst = (uint32_t)(p.sC[3] * EB);
 
   SeqCursor sc;
@@ -109,7 +125,7 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
       const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
       un[i] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
       dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
-      if (HAS_Z) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
+      if (HAS_Z && !MULTI) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
     }
   };
   fetch(t0);
@@ -126,7 +142,22 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
     for (int i = 0; i < TB; ++i) {
       uc[i] = un[i];
       dc[i] = dn[i];
-      zc[i] = HAS_Z ? zn[i] : 0.f;
+      zc[i] = (HAS_Z && !MULTI) ? zn[i] : 0.f;
+    }
+    // MULTI output pass: u (and z) of the steps this wave finishes after the block,
+    // i = gn + k nsg, reloaded now (they are in cache from the prefetch) so that the block's
+    // own u / z registers need not live until the end of the block.
+    float ucb[4] = {}, zcb[4] = {};
+    if constexpr (MULTI && FULL) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = gn + k * p.nsg;
+        if (i < TB) {
+          const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
+          ucb[k] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
+          if (HAS_Z) zcb[k] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
+        }
+      }
     }
     if (tb + TB < t1) fetch(tb + TB);
     // A sequence starts inside this block, or right after it (its predecessor's final
@@ -180,11 +211,15 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
           ssum += dt;
         } else {
           float y = (ys[0] + ys[1]) + (ys[2] + ys[3]);
-          y = fmaf(uu, Dv, y);
-          Buf<Tio>::store(rs_o, vo_o, r * st_o, y);
-          if (HAS_Z) {
-            const float zz = zc[i];
-            Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
+          if constexpr (MULTI) {
+            ysh[((tb - t0) / TB) & 1][gn][i][lane] = y;  // this group's share of y
+          } else {
+            y = fmaf(uu, Dv, y);
+            Buf<Tio>::store(rs_o, vo_o, r * st_o, y);
+            if (HAS_Z) {
+              const float zz = zc[i];
+              Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
+            }
           }
           if (GEN) {
             // Final states: of the sequence that owns step t when the next step starts a
@@ -193,11 +228,36 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
             const bool seq_end = varlen ? (blk_has_start && t + 1 == sc.pending) : (t == L - 1);
             if (seq_end && p.last_state != nullptr) {
               const int64_t row = varlen ? (int64_t)(sc.idx - 1) : b;
-              if (active) store_state<NS>(p.last_state + (row * p.D + d) * p.N, h, N);
+              if (active) store_state<NS>(p.last_state + (row * p.D + d) * p.N + s0, h, Nw);
             }
           }
           if ((i == TB - 1 || (GEN && t == L - 1)) && xck != nullptr) {
-            if (active) store_state<NS>(xck + (int64_t)(t / kCk) * xck_step, h, N);
+            if (active) store_state<NS>(xck + (int64_t)(t / kCk) * xck_step, h, Nw);
+          }
+        }
+      }
+      if constexpr (MULTI && FULL) {
+        // y of the block's steps: every wave wrote its share to LDS above (double-buffered
+        // by block parity, so one barrier per block suffices); wave gn now finishes the
+        // steps i = gn, gn + nsg, ...: groups summed in order 0..nsg-1, D u, gate, store.
+        const int par = ((tb - t0) / TB) & 1;
+        __syncthreads();
+        const int nsg = p.nsg;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int i = gn + k * nsg;
+          const int t = tb + i;
+          if (i >= TB || (GEN && t >= t1)) continue;  // wave-uniform
+          float y = ysh[par][0][i][lane];
+#pragma unroll
+          for (int q = 1; q < 4; ++q)
+            if (q < nsg) y += ysh[par][q][i][lane];
+          y = fmaf(ucb[k], Dv, y);
+          const uint32_t r = (uint32_t)(t - t0);
+          Buf<Tio>::store(rs_o, vo_o, r * st_o, y);
+          if (HAS_Z) {
+            const float zz = zcb[k];
+            Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
           }
         }
       }
@@ -205,9 +265,11 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
     if (general) block(std::true_type{}); else block(std::false_type{});
   }
   if (!FULL && active) {
-    store_state<NS>(p.ws_h + (ch * p.K + c) * p.N, h, N);
-    p.ws_s[ch * p.K + c] = ssum;
-    if (varlen) p.ws_r[ch * p.K + c] = seen_start ? 1 : 0;
+    store_state<NS>(p.ws_h + (ch * p.K + c) * p.N + s0, h, Nw);
+    if (gn == 0) {
+      p.ws_s[ch * p.K + c] = ssum;
+      if (varlen) p.ws_r[ch * p.K + c] = seen_start ? 1 : 0;
+    }
   }
 }
 
@@ -215,41 +277,42 @@ __global__ void __launch_bounds__(kWave) fwd_scan(FwdK p) {
 // Host-side launch helpers
 // ---------------------------------------------------------------------------------------
 
-template <typename Tio, typename Tbc, int NS, int DTM>
+template <typename Tio, typename Tbc, int NS, int DTM, bool MULTI>
 static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st, void* const* ev) {
   hipError_t e = hipSuccess;
   const dim3 grid = xcd_grid(k.Bsz * k.nDblk, k.K);
+  const dim3 block(MULTI ? (unsigned)(k.nsg * kWave) : (unsigned)kWave);
   if (k.K > 1) {
     // Summaries of chunks 0..K-2: the last chunk's summary is never used.
     const dim3 gsum = xcd_grid(k.Bsz * k.nDblk, k.K - 1);
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 0, DTM>), gsum, dim3(kWave), 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 0, DTM, MULTI>), gsum, block, 0, st, k);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_fwd_carry(k, st)) != hipSuccess) return e;
   }
   if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
   if (k.has_z)
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 2, DTM>), grid, dim3(kWave), 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 2, DTM, MULTI>), grid, block, 0, st, k);
   else
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 1, DTM>), grid, dim3(kWave), 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 1, DTM, MULTI>), grid, block, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return record_event(ev, 1, st);
 }
 
-template <typename Tio, typename Tbc, int NS>
+template <typename Tio, typename Tbc, int NS, bool MULTI>
 static hipError_t launch_dt(const FwdK& k, hipStream_t st, void* const* ev) {
   switch (dt_mode(k.has_bias, k.softplus)) {
-    case kDtRaw: return launch_scan_pair<Tio, Tbc, NS, kDtRaw>(k, st, ev);
-    case kDtBias: return launch_scan_pair<Tio, Tbc, NS, kDtBias>(k, st, ev);
-    default: return launch_scan_pair<Tio, Tbc, NS, kDtSoftplus>(k, st, ev);
+    case kDtRaw: return launch_scan_pair<Tio, Tbc, NS, kDtRaw, MULTI>(k, st, ev);
+    case kDtBias: return launch_scan_pair<Tio, Tbc, NS, kDtBias, MULTI>(k, st, ev);
+    default: return launch_scan_pair<Tio, Tbc, NS, kDtSoftplus, MULTI>(k, st, ev);
   }
 }
 
 template <typename Tio, typename Tbc>
 static hipError_t launch_bc(const FwdK& k, hipStream_t st, void* const* ev) {
-  if (k.N <= 8) return launch_dt<Tio, Tbc, 8>(k, st, ev);
-  if (k.N <= 16) return launch_dt<Tio, Tbc, 16>(k, st, ev);
-  if (k.N <= 32) return launch_dt<Tio, Tbc, 32>(k, st, ev);
-  return launch_dt<Tio, Tbc, 64>(k, st, ev);
+  if (k.N <= 8) return launch_dt<Tio, Tbc, 8, false>(k, st, ev);
+  if (k.N <= 16) return launch_dt<Tio, Tbc, 16, false>(k, st, ev);
+  if (k.N <= 32) return launch_dt<Tio, Tbc, 32, false>(k, st, ev);
+  return launch_dt<Tio, Tbc, 16, true>(k, st, ev);  // k.nsg groups of 16 states
 }
 
 template <typename Tio>
