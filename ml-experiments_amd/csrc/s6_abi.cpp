@@ -48,7 +48,7 @@ struct Plan {
   bool relayout_B, relayout_C;
   int64_t NP;  // padded dstate of relaid-out B / C
   size_t off_h, off_s, off_r, off_B, off_C, total_fwd;
-  size_t off_pB, off_pC, off_dA, off_dD, off_db, off_s12, total_bwd;
+  size_t off_pB, off_pC, off_dA, off_dD, off_db, total_bwd;
   int64_t nsg, NPr;  // backward: state groups of 16, partial row width
 };
 
@@ -121,9 +121,6 @@ Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, 
   off += p.has_D ? align256(rows * p.dim * 4) : 0;
   pl.off_db = off;
   off += p.has_delta_bias ? align256(rows * p.dim * 4) : 0;
-  pl.off_s12 = off;  // two [nsg, batch, seqlen, dim] fp32 buffers when dstate > 16
-  const size_t s12 = pl.nsg > 1 ? align256((size_t)(pl.nsg * p.batch * p.seqlen * p.dim) * 4) : 0;
-  off += 2 * s12;
   pl.total_bwd = off;
   return pl;
 }
@@ -963,9 +960,6 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.ws_dA = (float*)(ws + pl.off_dA);
     k.ws_dD = p.has_D ? (float*)(ws + pl.off_dD) : nullptr;
     k.ws_db = p.has_delta_bias ? (float*)(ws + pl.off_db) : nullptr;
-    const size_t s12 = pl.nsg > 1 ? align256((size_t)(pl.nsg * p.batch * p.seqlen * p.dim) * 4) : 0;
-    k.ws_s1 = pl.nsg > 1 ? (float*)(ws + pl.off_s12) : nullptr;
-    k.ws_s2 = pl.nsg > 1 ? (float*)(ws + pl.off_s12 + s12) : nullptr;
     k.K = pl.K; k.Lc = pl.Lc;
     k.nDblk = pl.nDblk; k.nJ = pl.nJ; k.nsg = pl.nsg; k.NPr = pl.NPr;
     k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;

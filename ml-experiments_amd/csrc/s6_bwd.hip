@@ -19,7 +19,6 @@
 //                dstate 16) so the segment's states fit in VGPRs.  dB / dC are reduced over the
 //                64 lanes with permlane swaps and DPP and written as one partial per wave;
 //                dA / dD / ddelta_bias as one partial per (batch, chunk).
-//   bwd_finish   (dstate > 16 only) du / ddelta from the per-state-group sums.
 //   bwd_reduce_* fixed-order sums of the partials (s6_misc.hip): the result is deterministic.
 #include <type_traits>
 
@@ -146,18 +145,20 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   }
 }
 
-// MULTI: dstate > 16.  Each wave handles one group of NS (16) states; the per-step sums
-// over states that du / dDelta need are written per group (ws_s1 / ws_s2) and combined by
-// bwd_finish.
+// MULTI: dstate > 16.  The workgroup holds one wave per group of NS (16) states of the same
+// channels and chunk (p.nsg waves).  After each segment the waves exchange their per-step
+// sums over states (sum lambda B, sum q A) through LDS, and wave gn finishes the steps
+// gn, gn + nsg, ...: groups summed in order 0..nsg-1, du, dDelta and the ddelta_bias share.
 template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI>
-__global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_scan(BwdK p) {
+__global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
+    __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_scan(BwdK p) {
   constexpr int SEG = kCk;  // steps per segment = checkpoint interval
   constexpr int HS = 8;     // states per half
   constexpr int NH = NS / HS;
   static_assert(NS % HS == 0, "dstate padding");
   constexpr int ES = Elem<Tio>::kSize;
   constexpr int EB = Elem<Tbc>::kSize;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
   const BlockPos bp = block_pos(p.Bsz * p.nDblk);
   const int64_t Dg = p.D / p.G;
   const int64_t b = bp.x / p.nDblk;
@@ -168,9 +169,10 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   const bool active = dloc < Dg;
   const int64_t d0 = g * Dg + j * kWave;
   const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int c = (int)(bp.y % p.K);
-  const int gn = MULTI ? (int)(bp.y / p.K) : 0;  // state group
-  const int s0 = gn * NS;                         // its first state
+  const int c = MULTI ? (int)bp.y : (int)(bp.y % p.K);
+  // State group of this wave, wave-uniform (an SGPR) so that the B / C rows stay scalar.
+  const int gn = MULTI ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)) : 0;
+  const int s0 = gn * NS;  // its first state
   const int t0 = c * (int)p.Lc;
   const int t1 = min(t0 + (int)p.Lc, (int)p.L);
   const int N = (int)p.N - s0;                    // states of the group (may exceed NS)
@@ -238,7 +240,12 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   constexpr bool LDS_A = !HAS_Z && DTM != kDtSoftplus;
   constexpr bool LDS_H = HAS_Z;
   static_assert(HS == 8, "two float4 per step");
-  __shared__ float4 sa[(LDS_A || LDS_H) ? SEG * 2 * kWave : 1];
+  constexpr int kSlice = SEG * 2 * kWave;  // float4 per wave: 16 KB
+  // MULTI: one dynamic slice per wave (p.nsg * 16 KB), which also carries the per-step sums
+  // the waves exchange once the segment's reverse sweeps are done.
+  __shared__ float4 sa_wave[(!MULTI && (LDS_A || LDS_H)) ? kSlice : 1];
+  extern __shared__ float4 sa_dyn[];
+  float4* const sa = MULTI ? sa_dyn + gn * kSlice : sa_wave;
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.
@@ -269,7 +276,12 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
   BCGroup<Tbc> bnx, cnx;
   bnx.template load<HS>(Bbase + (uint32_t)((nseg - 1) * SEG) * Bst);
 
+  const int nsg = MULTI ? p.nsg : 1;
+  const float* const sx0 = reinterpret_cast<const float*>(sa_dyn);  // MULTI: slice of group 0
   for (int s = nseg - 1; s >= 0; --s) {
+    // MULTI: every wave has read the previous segment's exchanged sums from all slices
+    // before this segment's recompute writes its own slice again.
+    if constexpr (MULTI) __syncthreads();
     const int ts = t0 + s * SEG;
     const int te = min(ts + SEG, t1);
     float uu[SEG], dt[SEG], dy[SEG], pre[SEG], hst[NS];
@@ -428,17 +440,30 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
         }
       }
     }
+    // MULTI: this group's per-step sums over states go to the wave's own slice (its rows
+    // are consumed by now); after the barrier wave gn finishes steps gn, gn + nsg, ...
+    float* const sx = reinterpret_cast<float*>(sa);  // [2][SEG][kWave] at the slice start
+    if constexpr (MULTI) {
+#pragma unroll
+      for (int i = 0; i < SEG; ++i) {
+        sx[i * kWave + lane] = s1[i];
+        sx[(SEG + i) * kWave + lane] = s2[i];
+      }
+      __syncthreads();
+    }
     // Per-step outputs of the segment.
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
-      if (MULTI) {  // this group's sums over states; du / ddelta are formed by bwd_finish
-        if (ts + i < te && active) {
-          const int64_t o = (((int64_t)gn * p.Bsz + b) * p.L + ts + i) * p.D + d;
-          p.ws_s1[o] = s1[i];
-          p.ws_s2[o] = s2[i];
-          dDacc = fmaf(dy[i], uu[i], dDacc);
+      if (MULTI) {
+        if (ts + i < te) dDacc = fmaf(dy[i], uu[i], dDacc);  // written by group 0 only
+        if (i % nsg != gn) continue;  // wave-uniform
+        float S1 = sx0[i * kWave + lane], S2 = sx0[(SEG + i) * kWave + lane];
+        for (int q = 1; q < nsg; ++q) {
+          S1 += sx0[q * (kSlice * 4) + i * kWave + lane];
+          S2 += sx0[q * (kSlice * 4) + (SEG + i) * kWave + lane];
         }
-        continue;
+        s1[i] = S1;
+        s2[i] = S2;
       }
       if (ts + i < te) {
         const uint32_t r = (uint32_t)(ts + i - t0);
@@ -447,8 +472,19 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
         if (DTM == kDtSoftplus) ddv *= softplus20_grad(pre[i]);
         Buf<Tio>::store(rs_du, vo_du, r * st_du, duv);
         Buf<Tio>::store(rs_dd, vo_dd, r * st_dd, ddv);
-        dDacc = fmaf(dy[i], uu[i], dDacc);
+        if (!MULTI) dDacc = fmaf(dy[i], uu[i], dDacc);
         dbacc += ddv;
+      }
+    }
+  }
+  // MULTI: the ddelta_bias shares of the groups' steps, summed by group 0 in group order.
+  if constexpr (MULTI) {
+    if (p.has_bias) {
+      __syncthreads();
+      reinterpret_cast<float*>(sa)[lane] = dbacc;
+      __syncthreads();
+      if (gn == 0) {
+        for (int q = 1; q < nsg; ++q) dbacc += sx0[q * (kSlice * 4) + lane];
       }
     }
   }
@@ -459,66 +495,8 @@ __global__ void __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int n = 0; n < NS; ++n)
       if (n < N) dAp[n] = dAacc[n];
     if (p.has_D && gn == 0) p.ws_dD[row * p.D + d] = dDacc;
-    if (p.has_bias && !MULTI) p.ws_db[row * p.D + d] = dbacc;
+    if (p.has_bias && gn == 0) p.ws_db[row * p.D + d] = dbacc;
   }
-}
-
-// dstate > 16: du = Delta S1 + D dy and dDelta = u S1 + S2 (times softplus'), with S1, S2 the
-// sums over all state groups of ws_s1 / ws_s2; also the ddelta_bias partials.  One wave per
-// (batch, 64 channels, chunk), lane = channel.
-template <typename Tio, int DTM, bool HAS_Z>
-__global__ void __launch_bounds__(kWave) bwd_finish(BwdK p) {
-  constexpr int ES = Elem<Tio>::kSize;
-  const int lane = threadIdx.x;
-  const BlockPos bp = block_pos(p.Bsz * p.nDblk);
-  const int64_t Dg = p.D / p.G;
-  const int64_t b = bp.x / p.nDblk;
-  const int64_t rem = bp.x % p.nDblk;
-  const int64_t g = rem / p.nJ;
-  const int64_t j = rem % p.nJ;
-  const int64_t dloc = j * kWave + lane;
-  const bool active = dloc < Dg;
-  const int64_t d0 = g * Dg + j * kWave;
-  const int64_t d = g * Dg + (active ? dloc : Dg - 1);
-  const int c = (int)bp.y;
-  const int t0 = c * (int)p.Lc;
-  const int t1 = min(t0 + (int)p.Lc, (int)p.L);
-  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
-  const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
-  auto rsrc = [&](const void* base, const int64_t* s) {
-    return make_rsrc((const char*)base + (b * s[0] + d0 * s[1] + (int64_t)t0 * s[2]) * ES);
-  };
-  auto voff = [&](const int64_t* s) { return active ? (uint32_t)(lane * s[1] * ES) : kOffDrop; };
-  const auto rs_u = rsrc(p.u, p.su), rs_d = rsrc(p.delta, p.sdl), rs_o = rsrc(p.dout, p.sdo);
-  const auto rs_du = rsrc(p.du, p.sdu), rs_dd = rsrc(p.ddelta, p.sddl);
-  const auto rs_z = rsrc(HAS_Z ? p.z : p.u, HAS_Z ? p.sz : p.su);
-  const uint32_t vo_u = voff(p.su), vo_d = voff(p.sdl), vo_o = voff(p.sdo), vo_du = voff(p.sdu);
-  const uint32_t vo_dd = voff(p.sddl), vo_z = HAS_Z ? voff(p.sz) : kOffDrop;
-  float dbacc = 0.f;
-  for (int t = t0; t < t1; ++t) {
-    const uint32_t r = (uint32_t)(t - t0);
-    const float uu = Buf<Tio>::load(rs_u, vo_u, r * (uint32_t)(p.su[2] * ES));
-    const float raw = Buf<Tio>::load(rs_d, vo_d, r * (uint32_t)(p.sdl[2] * ES));
-    float dy = Buf<Tio>::load(rs_o, vo_o, r * (uint32_t)(p.sdo[2] * ES));
-    if (HAS_Z) {
-      const float zz = Buf<Tio>::load(rs_z, vo_z, r * (uint32_t)(p.sz[2] * ES));
-      dy *= zz * sigmoidf_(zz);
-    }
-    float s1 = 0.f, s2 = 0.f;
-    for (int64_t gn = 0; gn < p.nsg; ++gn) {
-      const int64_t o = ((gn * p.Bsz + b) * p.L + t) * p.D + d;
-      s1 += p.ws_s1[o];
-      s2 += p.ws_s2[o];
-    }
-    const float dt = prep_dt<DTM>(raw, bias);
-    const float duv = fmaf(dt, s1, Dv * dy);
-    float ddv = fmaf(uu, s1, s2 * 0.69314718055994531f);  // Ap = A log2(e)
-    if (DTM == kDtSoftplus) ddv *= softplus20_grad(raw + bias);
-    Buf<Tio>::store(rs_du, vo_du, r * (uint32_t)(p.sdu[2] * ES), duv);
-    Buf<Tio>::store(rs_dd, vo_dd, r * (uint32_t)(p.sddl[2] * ES), ddv);
-    dbacc += ddv;
-  }
-  if (active && p.has_bias) p.ws_db[(b * p.K + c) * p.D + d] = dbacc;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -534,14 +512,15 @@ static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st, void* const* ev) {
     if ((e = launch_bwd_carry(k, st)) != hipSuccess) return e;
   }
   if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K * k.nsg),
-                     dim3(kWave), 0, st, k);
+  if (MULTI) {  // one workgroup of nsg waves per chunk, 16 KB of LDS per wave
+    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K),
+                       dim3((unsigned)(k.nsg * kWave)), (unsigned)(k.nsg * kCk * 2 * kWave * 16), st, k);
+  } else {
+    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K),
+                       dim3(kWave), 0, st, k);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if ((e = record_event(ev, 1, st)) != hipSuccess) return e;
-  if (MULTI) {
-    hipLaunchKernelGGL((bwd_finish<Tio, DTM, HAS_Z>), xcd_grid(nx, k.K), dim3(kWave), 0, st, k);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
   return launch_bwd_reduce(k, st);
 }
 

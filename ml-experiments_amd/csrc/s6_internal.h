@@ -76,8 +76,8 @@ struct BwdK {
   int32_t* ws_r; // [Bsz*D, K]        1 if a sequence starts inside the chunk (varlen only)
   float* ws_pB;  // [Bsz, G, nJ, L, NPr]  per-64-channel-block partial dB
   float* ws_pC;  // [Bsz, G, nJ, L, NPr]  per-64-channel-block partial dC
-  float* ws_s1;  // [nsg, Bsz, L, D]  dstate > 16: per-state-group sum of lambda B
-  float* ws_s2;  // [nsg, Bsz, L, D]  dstate > 16: per-state-group sum of q A
+  float* ws_s1;  // unused (kept so that the kernel-argument layout, and with it the
+  float* ws_s2;  // register allocation of the hot kernels, stays as measured)
   float* ws_dA;  // [Bsz*K, D, N]     per-(batch, chunk) partial dA
   float* ws_dD;  // [Bsz*K, D]        per-(batch, chunk) partial dD
   float* ws_db;  // [Bsz*K, D]        per-(batch, chunk) partial ddelta_bias
