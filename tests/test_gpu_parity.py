@@ -411,18 +411,19 @@ def test_random_shapes_forward_and_backward(case):
     _grads_vs_ref(inp, layout=layout)
 
 
-@pytest.mark.parametrize("z,bias,layout,L", [(False, False, "view", 203), (True, True, "view", 203),
-                                             (True, False, "contiguous", 203),
-                                             (True, True, "view", 8), (False, True, "view", 5),
-                                             (True, False, "view", 64)])
-def test_native_module_contract(z, bias, layout, L):
+@pytest.mark.parametrize("z,bias,layout,L,N", [(False, False, "view", 203, 16), (True, True, "view", 203, 16),
+                                               (True, False, "contiguous", 203, 16),
+                                               (True, True, "view", 8, 16), (False, True, "view", 5, 16),
+                                               (True, False, "view", 64, 16), (True, True, "view", 203, 48)])
+def test_native_module_contract(z, bias, layout, L, N):
     """s6scan.selective_scan_cuda against the drop-in op, called the way the reference's
     Python calls its native module: fwd with 4-D B/C, last_state read as x[:, :, -1, 1::2],
     bwd with the saved x and out, a preallocated dz, and recompute_out_z.  Lengths of one
     (partial or full) segment and a multiple of 8 check that mirroring the final state into
-    the last segment's odd slots leaves what the backward reads intact."""
+    the last segment's odd slots leaves what the backward reads intact; dstate 48 runs the
+    state-group kernels on that strided checkpoint layout."""
     from s6scan import selective_scan_cuda as ssc
-    inp = gen(2, L, 96, 16, torch.bfloat16, seed=41, G=2, z=z, bias=bias)
+    inp = gen(2, L, 96, N, torch.bfloat16, seed=41, G=2, z=z, bias=bias)
     args, kw = call(inp, layout, DEV)
     u, delta, A, B, C = args
     B4, C4 = (B.unsqueeze(1), C.unsqueeze(1)) if B.dim() == 3 else (B, C)
@@ -430,7 +431,7 @@ def test_native_module_contract(z, bias, layout, L):
     res = ssc.fwd(u, delta, A, B4, C4, Dv, zz, db, sp)
     out, x = res[0], res[1]
     assert len(res) == (3 if z else 2)
-    assert x.shape == (2, 96, -(-L // 8), 32) and x.dtype == torch.float32
+    assert x.shape == (2, 96, -(-L // 8), 2 * N) and x.dtype == torch.float32
     want_out, want_ls = s6scan.selective_scan_fn(*args, **kw)
     got_out = res[2] if z else out
     assert torch.equal(got_out, want_out)
