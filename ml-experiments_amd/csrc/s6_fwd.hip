@@ -29,9 +29,14 @@ namespace s6 {
 // D u, gate and store.  This keeps every wave at the register footprint of 16 states; at
 // 17-32 states one wave holding them all measured faster (2 groups do not pay for the
 // duplicated per-step work and the barrier).
+// Occupancy target: 4 waves per SIMD (<= 128 VGPRs) for MULTI and for the z-gated softplus
+// output pass at 16 states, which the compiler otherwise lays out at 129 VGPRs (3 waves;
+// measured 5% slower).  The raw / bias z-gated variants would spill at 128 and keep the
+// default.
 template <typename Tio, typename Tbc, int NS, int MODE, int DTM, bool MULTI>
 __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
-    __attribute__((amdgpu_waves_per_eu(MULTI ? 4 : 1))) fwd_scan(FwdK p) {
+    __attribute__((amdgpu_waves_per_eu((MULTI || (MODE == 2 && DTM == kDtSoftplus && NS <= 16)) ? 4 : 1)))
+    fwd_scan(FwdK p) {
   constexpr bool FULL = MODE != 0;
   constexpr bool HAS_Z = MODE == 2;
   constexpr int TB = kCk;  // steps per unrolled block = checkpoint interval
