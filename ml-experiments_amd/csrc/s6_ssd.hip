@@ -85,8 +85,14 @@ __global__ void __launch_bounds__(kWave) ssd_cumsum(SsdK k) {
 // their weights) go to registers while the MFMAs of slice i run; the registers are written,
 // transposed and weighted, to the other half of a double LDS buffer, one barrier per slice.
 // (With a single buffer, when two would not fit in 64 KB, a second barrier guards it.)
+// Occupancy target of 4 waves per SIMD for headdim 64 x dstate 128 (Mamba-2's default),
+// which the compiler otherwise lays out at 140-144 registers (3 waves; the 4-wave layout
+// measured 172 -> 141 us), and for the small tiles it changes nothing for.  Larger tiles keep
+// the default: at 128 registers they would spill.
 template <typename T, int P, int N, int MODE>
-__global__ void __launch_bounds__(kThreads) ssd_chunk_state(SsdK k) {
+__global__ void __launch_bounds__(kThreads)
+    __attribute__((amdgpu_waves_per_eu((P * N <= 4096 || (P == 64 && N == 128)) ? 4 : 1)))
+    ssd_chunk_state(SsdK k) {
   typedef Mma<T> M;
   typedef typename M::Raw Raw;
   constexpr int VE = M::kVe;

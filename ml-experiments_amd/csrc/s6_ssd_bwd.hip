@@ -393,8 +393,13 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
 // slice.  The next head's matrix slice, A fragments and cumsums are loaded while the current
 // head computes; the matrix goes transposed (dstate-major, K = headdim contiguous) into a
 // double LDS buffer written with lanes along headdim, so the 2-byte writes do not collide.
+// Occupancy target of 4 waves per SIMD for MODE 5 at headdim 64 x dstate 128 with 16-bit
+// inputs, which fits it in 121 registers without spilling (the compiler's own layout takes
+// 144, 3 waves); MODE 4 and fp32 inputs would spill at that budget and keep the default.
 template <typename T, int P, int N, int MODE>
-__global__ void __launch_bounds__(kThreads) ssd_bwd_rows(SsdK k) {
+__global__ void __launch_bounds__(kThreads)
+    __attribute__((amdgpu_waves_per_eu((MODE == 5 && P == 64 && N == 128 && sizeof(T) == 2) ? 4 : 1)))
+    ssd_bwd_rows(SsdK k) {
   typedef Mma<T> M;
   typedef typename M::Raw Raw;
   typedef typename M::Frag Frag;
