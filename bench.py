@@ -61,7 +61,8 @@ def parse():
 
 
 def cpu_model():
-    """The host CPU's model name (the survey asks for it next to the CPU baseline)."""
+    """The host CPU's model name, reported next to the CPU baseline so that its figure can be
+    read against the hardware it ran on."""
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
