@@ -144,6 +144,15 @@ int s6_validate_problem(const S6Problem* p);
 int s6_validate_fwd(const S6FwdArgs* a);
 int s6_validate_bwd(const S6BwdArgs* a);
 
+/* Host-only check of packed-varlen offsets held in HOST memory (a copy of the device
+ * vector passed as cu_seqlens): nseq >= 1, cu[0] == 0, non-decreasing, cu[nseq] == seqlen.
+ * Returns S6_E_INVALID with a message naming the first violation.  s6_fwd / s6_bwd cannot
+ * read device memory before launching, so a caller passing device offsets it has not
+ * checked this way gets unspecified results for a malformed vector (the kernels still keep
+ * every store inside the output tensors).  Same convention as the reference's varlen
+ * chunked scan (ssd_combined.py:576-577, ssd_state_passing.py:76-78). */
+int s6_validate_cu_seqlens(const int32_t* cu_host, int64_t nseq, int64_t seqlen);
+
 /* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */
 int64_t s6_num_checkpoints(const S6Problem* p);
 

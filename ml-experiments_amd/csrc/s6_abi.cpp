@@ -795,6 +795,22 @@ int s6_validate_problem(const S6Problem* p) {
   return ok();
 }
 
+int s6_validate_cu_seqlens(const int32_t* cu, int64_t nseq, int64_t seqlen) {
+  if (cu == nullptr) return fail(S6_E_INVALID, "cu_seqlens must not be NULL");
+  if (nseq < 1 || nseq > (int64_t)INT32_MAX - 1)
+    return fail(S6_E_INVALID, "cu_seqlens must hold nseq + 1 offsets with 1 <= nseq < 2^31-1, got nseq %lld",
+                (long long)nseq);
+  if (cu[0] != 0) return fail(S6_E_INVALID, "cu_seqlens[0] must be 0, got %d", cu[0]);
+  for (int64_t i = 1; i <= nseq; ++i)
+    if (cu[i] < cu[i - 1])
+      return fail(S6_E_INVALID, "cu_seqlens must be non-decreasing: cu_seqlens[%lld] = %d < cu_seqlens[%lld] = %d",
+                  (long long)i, cu[i], (long long)(i - 1), cu[i - 1]);
+  if ((int64_t)cu[nseq] != seqlen)
+    return fail(S6_E_INVALID, "cu_seqlens[%lld] must equal seqlen %lld, got %d", (long long)nseq,
+                (long long)seqlen, cu[nseq]);
+  return ok();
+}
+
 int64_t s6_num_checkpoints(const S6Problem* p) {
   if (p == nullptr || p->seqlen < 1) return 0;
   return ceil_div(p->seqlen, s6::kCk);

@@ -232,8 +232,11 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
             // step.  The wave-uniform conditions are tested before the per-lane one.
             const bool seq_end = varlen ? (blk_has_start && t + 1 == sc.pending) : (t == L - 1);
             if (seq_end && p.last_state != nullptr) {
+              // Sequence row of the final state; a row outside [0, nseq) can only come
+              // from offsets the host validation rejects, and is never stored.
               const int64_t row = varlen ? (int64_t)(sc.idx - 1) : b;
-              if (active) store_state<NS>(p.last_state + (row * p.D + d) * p.N + s0, h, Nw);
+              const bool row_ok = !varlen || (row >= 0 && row < p.nseq);
+              if (active && row_ok) store_state<NS>(p.last_state + (row * p.D + d) * p.N + s0, h, Nw);
             }
           }
           if ((i == TB - 1 || (GEN && t == L - 1)) && xck != nullptr) {

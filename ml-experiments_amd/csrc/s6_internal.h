@@ -31,10 +31,15 @@ __device__ inline bool range_has_start(const int32_t* cu, int32_t nseq, int64_t 
 }
 
 // Bit i set when a sequence starts at step ts + i, for i in [0, te - ts), te - ts <= 32.
+// Offsets outside [ts, te) set no bit, so a vector that is not non-decreasing (which the
+// host rejects before launching) cannot produce an out-of-range shift.
 __device__ inline uint32_t start_mask(const int32_t* cu, int32_t nseq, int64_t ts, int64_t te) {
   SeqCursor s = seq_cursor_at(cu, nseq, ts);
   uint32_t m = 0;
-  for (int32_t i = s.idx; i <= nseq && (int64_t)cu[i] < te; ++i) m |= 1u << (uint32_t)(cu[i] - ts);
+  for (int32_t i = s.idx; i <= nseq && (int64_t)cu[i] < te; ++i) {
+    const int64_t off = (int64_t)cu[i] - ts;
+    if (off >= 0 && off < 32) m |= 1u << (uint32_t)off;
+  }
   return m;
 }
 

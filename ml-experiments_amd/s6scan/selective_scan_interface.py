@@ -42,6 +42,19 @@ def _strides(t, n):
     return tuple(t.stride())
 
 
+def check_cu_seqlens(cu_seqlens, seqlen):
+    """Contents of packed-varlen offsets: cu[0] == 0, non-decreasing, cu[-1] == seqlen (the
+    convention of the reference's varlen chunked scan, ssd_combined.py:576-577 and
+    ssd_state_passing.py:76-78).  Reads the nseq + 1 offsets to the host once (a device
+    synchronisation) and checks them with the library's host-only validator; a malformed
+    vector raises ValueError and is never passed to a kernel."""
+    host = cu_seqlens.detach().to("cpu", torch.int32).contiguous()
+    rc = _lib.LIB.s6_validate_cu_seqlens(ctypes.c_void_p(host.data_ptr()), host.numel() - 1,
+                                         int(seqlen))
+    if rc != _lib.OK:
+        raise ValueError(f"s6scan: {_lib.last_error()}")
+
+
 def check_inputs(u, delta, A, B, C, D=None, z=None, delta_bias=None, cu_seqlens=None):
     """Shape/dtype/device checks of the reference contract; returns the problem tuple
     (batch, dim, seqlen, dstate, ngroups, nseq).  Pure host logic: runs without a GPU."""
@@ -98,6 +111,7 @@ def check_inputs(u, delta, A, B, C, D=None, z=None, delta_bias=None, cu_seqlens=
         if cu_seqlens.dim() != 1 or cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() < 2:
             raise ValueError("cu_seqlens must be an int32 vector [nseq+1]")
         nseq = cu_seqlens.numel() - 1
+        check_cu_seqlens(cu_seqlens, seqlen)
     if dstate > _lib.MAX_DSTATE_FWD:
         raise NotImplementedError(f"s6scan: dstate {dstate} > {_lib.MAX_DSTATE_FWD} is not supported")
     tensors = [t for t in (u, delta, A, B, C, D, z, delta_bias, cu_seqlens) if t is not None]

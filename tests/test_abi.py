@@ -221,3 +221,35 @@ def test_conv_workspace_holds_one_partial_row_per_block():
     big = LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(seqlen=1 << 16)))
     assert small < big <= 2 * 256 * row + 256 + 64 * row
     assert LIB.s6_causal_conv1d_bwd_workspace_bytes(ctypes.byref(conv_prob(width=9))) == 0
+
+
+def _validate_cu(values, seqlen):
+    arr = (ctypes.c_int32 * len(values))(*values)
+    return _lib.LIB.s6_validate_cu_seqlens(ctypes.cast(arr, ctypes.c_void_p), len(values) - 1,
+                                           seqlen)
+
+
+@pytest.mark.parametrize("values,msg", [
+    ([10, 100], "cu_seqlens[0] must be 0"),                # does not start at 0
+    ([0, 60, 50, 100], "non-decreasing"),                  # not monotone
+    ([0, 50], "must equal seqlen 100"),                    # does not end at seqlen
+    ([0, 100, 120], "must equal seqlen 100"),              # runs past the end
+    ([0, -5, 100], "non-decreasing"),
+    ([0], "nseq"),                                         # no sequence
+])
+def test_cu_seqlens_validator_rejects(values, msg):
+    """Host-only check of packed-varlen offsets (the reference's varlen convention,
+    ssd_combined.py:576-577): malformed vectors return S6_E_INVALID and are never launched."""
+    assert _validate_cu(values, 100) == _lib.E_INVALID
+    assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("values", [[0, 100], [0, 0, 100], [0, 40, 40, 100, 100], [0, 1, 2, 100]])
+def test_cu_seqlens_validator_accepts(values):
+    # empty sequences (repeated offsets) are allowed, as in the reference's seq_idx form
+    assert _validate_cu(values, 100) == _lib.OK
+    assert _lib.last_error() == ""
+
+
+def test_cu_seqlens_validator_null():
+    assert _lib.LIB.s6_validate_cu_seqlens(None, 1, 100) == _lib.E_INVALID

@@ -89,3 +89,28 @@ def test_workload_generators_match_declared_shapes():
     assert int(cu[-1]) == v["x"].shape[1]
     assert CONFIGS[1].algorithmic_bytes() == 210256896
     assert CONFIGS[0].algorithmic_bytes() == 1720832
+
+
+@pytest.mark.parametrize("cu,msg", [
+    ([10, 100], r"cu_seqlens\[0\] must be 0"),
+    ([0, 60, 50, 100], "non-decreasing"),
+    ([0, 50], "must equal seqlen 100"),
+])
+def test_malformed_cu_seqlens_rejected_before_launch(cu, msg):
+    """check_inputs reads the offsets once and rejects a vector that does not start at 0, is
+    not non-decreasing or does not end at seqlen (ssd_combined.py:576-577,
+    ssd_state_passing.py:76-78): such a vector never reaches a kernel."""
+    u, dl, A, Bm, Cm = small(B=1, L=100)
+    with pytest.raises(ValueError, match=msg):
+        s6scan.check_inputs(u, dl, A, Bm, Cm, cu_seqlens=torch.tensor(cu, dtype=torch.int32))
+    # the public entry point raises the same error (before any device check)
+    with pytest.raises(ValueError, match=msg):
+        s6scan.selective_scan_fn(u, dl, A, Bm, Cm, cu_seqlens=torch.tensor(cu, dtype=torch.int32))
+
+
+def test_wellformed_cu_seqlens_accepted():
+    # the offsets pass; the only remaining complaint is the CPU device (no fallback)
+    u, dl, A, Bm, Cm = small(B=1, L=100)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        s6scan.check_inputs(u, dl, A, Bm, Cm,
+                            cu_seqlens=torch.tensor([0, 30, 30, 100], dtype=torch.int32))
