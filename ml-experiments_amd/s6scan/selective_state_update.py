@@ -35,41 +35,42 @@ def _st(t, n):
     return tuple(t.stride()) if t is not None else (0,) * n
 
 
+# Rank of each argument without a head axis, and where the head (or group) axis of size 1
+# goes when it is absent: the reference accepts both forms of every argument.
+_HEADLESS = {"state": (3, 1), "x": (2, 1), "dt": (2, 1), "A": (2, 0), "B": (2, 1), "C": (2, 1),
+             "D": (1, 0), "z": (2, 1), "dt_bias": (1, 0)}
+
+
+def _with_heads(name, t):
+    if t is None:
+        return None
+    rank, axis = _HEADLESS[name]
+    return t.unsqueeze(axis) if t.dim() == rank else t
+
+
+def _require(ok, what):
+    # shape errors are AssertionErrors, as in the reference wrapper
+    if not ok:
+        raise AssertionError(f"selective_state_update: {what}")
+
+
 def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
                            dt_softplus=False):
     has_heads = state.dim() > 3
-    if state.dim() == 3:
-        state = state.unsqueeze(1)
-    if x.dim() == 2:
-        x = x.unsqueeze(1)
-    if dt.dim() == 2:
-        dt = dt.unsqueeze(1)
-    if A.dim() == 2:
-        A = A.unsqueeze(0)
-    if B.dim() == 2:
-        B = B.unsqueeze(1)
-    if C.dim() == 2:
-        C = C.unsqueeze(1)
-    if D is not None and D.dim() == 1:
-        D = D.unsqueeze(0)
-    if z is not None and z.dim() == 2:
-        z = z.unsqueeze(1)
-    if dt_bias is not None and dt_bias.dim() == 1:
-        dt_bias = dt_bias.unsqueeze(0)
+    state, x, dt, A, B, C, D, z, dt_bias = (
+        _with_heads(n, t) for n, t in zip(("state", "x", "dt", "A", "B", "C", "D", "z", "dt_bias"),
+                                          (state, x, dt, A, B, C, D, z, dt_bias)))
     batch, nheads, dim, dstate = state.shape
-    assert x.shape == (batch, nheads, dim)
-    assert dt.shape == x.shape
-    assert A.shape == (nheads, dim, dstate)
     ngroups = B.shape[1]
-    assert nheads % ngroups == 0, "nheads must be divisible by ngroups"
-    assert B.shape == (batch, ngroups, dstate)
-    assert C.shape == B.shape
-    if D is not None:
-        assert D.shape == (nheads, dim)
-    if z is not None:
-        assert z.shape == x.shape
-    if dt_bias is not None:
-        assert dt_bias.shape == (nheads, dim)
+    want = {"x": (batch, nheads, dim), "dt": (batch, nheads, dim), "z": (batch, nheads, dim),
+            "A": (nheads, dim, dstate), "B": (batch, ngroups, dstate),
+            "C": (batch, ngroups, dstate), "D": (nheads, dim), "dt_bias": (nheads, dim)}
+    for name, t in (("x", x), ("dt", dt), ("A", A), ("B", B), ("C", C), ("D", D), ("z", z),
+                    ("dt_bias", dt_bias)):
+        if t is not None:
+            _require(tuple(t.shape) == want[name],
+                     f"{name} has shape {tuple(t.shape)}, expected {want[name]}")
+    _require(nheads % ngroups == 0, "nheads must be divisible by ngroups")
     if not state.is_cuda:
         raise RuntimeError("selective_state_update: tensors must be on a ROCm device (no CPU path)")
     for t, name in ((state, "state"), (x, "x"), (B, "B")):

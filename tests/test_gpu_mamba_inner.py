@@ -105,6 +105,62 @@ def test_conv_backward_long_sequence_reduces_partials_in_order():
     assert_grad_close(r1[2], gb, torch.float32, "dbias")
 
 
+def test_conv_module_arities_as_each_reference_file_calls_them():
+    """The two copies of the reference's interface file call the conv module with different
+    argument lists: the ops copy with the newer ones (selective_scan_interface.py:187-189,
+    299-301: fwd with 7 arguments, bwd with 10 returning 4 values) and the copy zoology's
+    Mamba imports (mamba_ssm/selective_scan_interface.py:181, 288-290, 321: fwd with 5, bwd with
+    7 returning 3 values, causal_conv1d_fn with the activation 4th).  s6scan.causal_conv1d
+    serves the first, s6scan.causal_conv1d_legacy the second; both must equal the reference's
+    nn.Conv1d path and its autograd."""
+    from s6scan import causal_conv1d as conv_new
+    from s6scan import causal_conv1d_legacy as conv_old
+
+    g = torch.Generator().manual_seed(21)
+    batch, dim, L, W = 2, 160, 257, 4
+    xz = torch.randn(batch, L, 2 * dim, generator=g).to(torch.bfloat16)
+    x = xz.to(DEV).mT[:, :dim]                       # x half of a channel-last xz, as in the block
+    xr = xz.mT[:, :dim].double()
+    w = torch.randn(dim, W, generator=g) * 0.5
+    b = torch.randn(dim, generator=g)
+    dout = torch.randn(batch, L, dim, generator=g).to(torch.bfloat16)
+    wg, bg, doutg = w.to(DEV), b.to(DEV), dout.to(DEV).mT
+
+    ref = causal_conv1d_ref(xr, w.double(), b.double(), "silu")
+    xl = xr.clone().requires_grad_(True)
+    wl = w.double().requires_grad_(True)
+    bl = b.double().requires_grad_(True)
+    gx, gw, gb = torch.autograd.grad(
+        (causal_conv1d_ref(xl, wl, bl, "silu") * dout.mT.double()).sum(), (xl, wl, bl))
+
+    # ops copy: conv1d_out = causal_conv1d_fwd(x, w, b, None, None, None, True)
+    out_new = conv_new.causal_conv1d_fwd(x, wg, bg, None, None, None, True)
+    # Mamba's copy: conv1d_out = causal_conv1d_fwd(x, w, b, None, True)
+    out_old = conv_old.causal_conv1d_fwd(x, wg, bg, None, True)
+    assert torch.equal(out_new, out_old)
+    assert_out_close(out_old, ref, torch.bfloat16, "conv out (5-argument fwd)")
+
+    # ops copy: dx, dw, db, *_ = causal_conv1d_bwd(x, w, b, dout, None, None, None, dx, False, True)
+    dx_new = torch.empty_like(x)
+    res_new = conv_new.causal_conv1d_bwd(x, wg, bg, doutg, None, None, None, dx_new, False, True)
+    assert len(res_new) == 4 and res_new[0] is dx_new
+    # Mamba's copy: dx, dw, db = causal_conv1d_bwd(x, w, b, dout, None, dx, True)
+    dx_old = torch.empty_like(x)
+    res_old = conv_old.causal_conv1d_bwd(x, wg, bg, doutg, None, dx_old, True)
+    assert len(res_old) == 3 and res_old[0] is dx_old
+    for a_new, a_old in zip(res_new[:3], res_old):
+        assert torch.equal(a_new, a_old)
+    assert_grad_close(res_old[0], gx, torch.bfloat16, "dx (7-argument bwd)")
+    assert_grad_close(res_old[1], gw, torch.bfloat16, "dweight (7-argument bwd)")
+    assert_grad_close(res_old[2], gb, torch.bfloat16, "dbias (7-argument bwd)")
+
+    # causal_conv1d_fn: activation 4th (Mamba's copy, :321) and 5th (mamba.py:163-169)
+    y_old = conv_old.causal_conv1d_fn(x, wg, bg, "silu")
+    y_new = conv_new.causal_conv1d_fn(x, wg, bg, None, "silu")
+    assert torch.equal(y_old, y_new)
+    assert_out_close(y_old, ref, torch.bfloat16, "causal_conv1d_fn")
+
+
 def test_conv_fn_autograd_without_bias():
     g = torch.Generator().manual_seed(9)
     x = torch.randn(2, 100, 32, generator=g)

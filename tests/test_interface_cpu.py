@@ -114,3 +114,27 @@ def test_wellformed_cu_seqlens_accepted():
     with pytest.raises(RuntimeError, match="ROCm devices only"):
         s6scan.check_inputs(u, dl, A, Bm, Cm,
                             cu_seqlens=torch.tensor([0, 30, 30, 100], dtype=torch.int32))
+
+
+def test_legacy_conv_module_signatures():
+    """s6scan.causal_conv1d_legacy has the argument lists of the conv module calls in the
+    interface file zoology's Mamba imports (mamba_ssm/selective_scan_interface.py:181,
+    288-290, 321); s6scan.causal_conv1d those of the ops copy (ops/...:187-189, 299-301)."""
+    import inspect
+
+    from s6scan import causal_conv1d as new
+    from s6scan import causal_conv1d_legacy as old
+
+    def names(f):
+        return list(inspect.signature(f).parameters)
+
+    assert names(old.causal_conv1d_fwd) == ["x", "weight", "bias", "seq_idx", "silu_activation"]
+    assert names(old.causal_conv1d_bwd) == ["x", "weight", "bias", "dout", "seq_idx", "dx",
+                                            "silu_activation"]
+    assert len(names(new.causal_conv1d_fwd)) == 7 and len(names(new.causal_conv1d_bwd)) == 10
+    # a CPU tensor still raises (no fallback) through either arity
+    x = torch.randn(1, 4, 8)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        old.causal_conv1d_fwd(x, torch.randn(4, 3), None, None, True)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        old.causal_conv1d_fn(x, torch.randn(4, 3), None, "silu")
