@@ -31,7 +31,9 @@ def _load():
         _lib.s6o_fwd.argtypes = [i64] * 5 + [vp] * 8 + [ctypes.c_int, vp, ctypes.c_int32, vp, vp]
         _lib.s6o_bwd.argtypes = ([i64] * 5 + [vp] * 8 + [ctypes.c_int, vp, ctypes.c_int32]
                                  + [vp] * 9)
+        _lib.s6o_fwd64.argtypes = _lib.s6o_fwd.argtypes
         _lib.s6o_fwd.restype = None
+        _lib.s6o_fwd64.restype = None
         _lib.s6o_bwd.restype = None
     return _lib
 
@@ -67,6 +69,24 @@ def fwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False
     ls = torch.empty(nseq if nseq else Bsz, Dm, N, dtype=torch.float32)
     lib.s6o_fwd(Bsz, Dm, L, N, G, _p(uu), _p(dl), _p(AA), _p(BB), _p(CC), _p(Dv), _p(zz),
                 _p(bb), int(bool(delta_softplus)), _p(cu), nseq, _p(out), _p(ls))
+    return out, ls
+
+
+def fwd64(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+          cu_seqlens=None):
+    """The recurrence in float64 from the fp32-cast inputs: (out, last_state) as float64
+    tensors -- the exact value that fp32 results are measured against."""
+    lib = _load()
+    uu, dl, AA, BB, CC = _f(u), _f(delta), _f(A), _bc4(B), _bc4(C)
+    Dv, zz, bb = _f(D), _f(z), _f(delta_bias)
+    Bsz, Dm, L = uu.shape
+    N, G = AA.shape[1], BB.shape[1]
+    cu = None if cu_seqlens is None else cu_seqlens.to(torch.int32).contiguous()
+    nseq = 0 if cu is None else cu.numel() - 1
+    out = torch.empty(Bsz, Dm, L, dtype=torch.float64)
+    ls = torch.empty(nseq if nseq else Bsz, Dm, N, dtype=torch.float64)
+    lib.s6o_fwd64(Bsz, Dm, L, N, G, _p(uu), _p(dl), _p(AA), _p(BB), _p(CC), _p(Dv), _p(zz),
+                  _p(bb), int(bool(delta_softplus)), _p(cu), nseq, _p(out), _p(ls))
     return out, ls
 
 

@@ -192,3 +192,54 @@ void s6o_bwd(int64_t Bsz, int64_t D, int64_t L, int64_t N, int64_t G, const floa
   }
   free(accB); free(accC); free(st);
 }
+
+/* The same recurrence evaluated in double precision from the fp32 inputs (no rounding to
+ * fp32 anywhere): the exact value that the fp32 paths are compared with.  Same arguments as
+ * s6o_fwd; out / last_state are double.  Pinned against oracle/brute64.py scan_fwd64. */
+void s6o_fwd64(int64_t Bsz, int64_t D, int64_t L, int64_t N, int64_t G, const float* u,
+               const float* delta, const float* A, const float* Bm, const float* Cm,
+               const float* Dv, const float* z, const float* bias, int softplus,
+               const int32_t* cu, int32_t nseq, double* out, double* last_state) {
+  unsigned char* st = (unsigned char*)malloc((size_t)L);
+  starts_mask(L, cu, nseq > 0 ? nseq : 0, st);
+  const int64_t Dg = D / G;
+  if (last_state && nseq > 0)
+    memset(last_state, 0, (size_t)(nseq * D * N) * sizeof(double));
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t ch = 0; ch < Bsz * D; ++ch) {
+    const int64_t b = ch / D, d = ch % D, g = d / Dg;
+    double* x = (double*)calloc((size_t)N, sizeof(double));
+    const float* uu = u + ch * L;
+    const float* Bb = Bm + (b * G + g) * N * L;
+    const float* Cb = Cm + (b * G + g) * N * L;
+    int32_t seq = -1;
+    for (int64_t t = 0; t < L; ++t) {
+      if (st[t]) {
+        memset(x, 0, (size_t)N * sizeof(double));
+        ++seq;
+        if (nseq > 0)
+          while (seq + 1 < nseq && cu[seq + 1] <= t) ++seq;
+      }
+      double dt = (double)delta[ch * L + t] + (bias ? (double)bias[d] : 0.0);
+      if (softplus) dt = dt <= 20.0 ? log1p(exp(dt)) : dt;
+      double y = 0.0;
+      for (int64_t n = 0; n < N; ++n) {
+        x[n] = exp(dt * A[d * N + n]) * x[n] + dt * uu[t] * Bb[n * L + t];
+        y += x[n] * Cb[n * L + t];
+      }
+      if (Dv) y += (double)uu[t] * Dv[d];
+      if (z) {
+        const double zz = z[ch * L + t];
+        y *= zz / (1.0 + exp(-zz));
+      }
+      out[ch * L + t] = y;
+      const int end = (t == L - 1) || (nseq > 0 && st[t + 1]);
+      if (last_state && end) {
+        const int64_t row = nseq > 0 ? ((int64_t)seq * D + d) : ch;
+        for (int64_t n = 0; n < N; ++n) last_state[row * N + n] = x[n];
+      }
+    }
+    free(x);
+  }
+  free(st);
+}

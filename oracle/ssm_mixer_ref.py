@@ -13,6 +13,15 @@ mixer's channel-last ``[B, L, *]`` layout:
 * ``state = dA[:, i] * state + dB_x[:, i]``; ``y[:, i] = einsum('bis,bs->bi')`` (1227-1238)
 * ``y = y + x_conv * D``; ``y = y * silu(z)``                                   (1241-1242)
 
+One deliberate departure from the reference's text: backbone.py:1220-1222 forms
+``dB = dt[:, :, :, None] * B_param[:, None, :, :]``, i.e. ``[B, L, I, 1] * [B, 1, L, N]``.
+That broadcast fails unless ``I == L``, and when ``I == L`` it pairs channel i with the B row
+of *time step* i, which is not the S6 recurrence the mixer documents (dB = dt * B,
+``[B, L, I, N]``, backbone.py:1214-1216) nor what ``selective_scan_ref`` computes
+(selective_scan_interface.py:130-134).  This restatement uses ``B_param[:, :, None, :]``
+(``[B, L, 1, N]``), the broadcast that yields the documented ``[B, L, I, N]`` shape; with
+it the two restatements agree (``tests/test_oracle.py``).
+
 The reference keeps the state in ``x.dtype``; ``state_dtype`` selects it (None = the input
 dtype, as the reference; torch.float32 = the fp32 state the HIP kernel keeps).  Pinned by
 ``tests/test_oracle.py`` against ``selective_scan_ref`` (itself pinned by the float64 brute

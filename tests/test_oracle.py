@@ -248,6 +248,18 @@ def test_c_oracle_backward_matches_brute64(kw):
                                    err_msg=k)
 
 
+@pytest.mark.parametrize("kw", CASES)
+def test_c_oracle_float64_forward_matches_brute64(kw):
+    """The C float64 forward (the exact value fp32 results are measured against) equals the
+    independent NumPy float64 brute force."""
+    u, dl, A, Bm, Cm, Dv, z, b = _inputs(**kw, dtype=torch.float32, seed=34)
+    sp = b is not None
+    co, cls = c_oracle.fwd64(u, dl, A, Bm, Cm, Dv, z, b, sp)
+    h = scan_fwd64(_np(u), _np(dl), _np(A), _np(Bm), _np(Cm), _np(Dv), _np(z), _np(b), sp)
+    np.testing.assert_allclose(co.numpy(), h["out"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(cls.numpy(), h["last_state"], rtol=1e-12, atol=1e-12)
+
+
 def test_c_oracle_varlen():
     u, dl, A, Bm, Cm, Dv, z, b = _inputs(B=1, D=4, L=60, N=6, z=True, bias=True, dtype=torch.float32,
                                          seed=33)
@@ -257,6 +269,11 @@ def test_c_oracle_varlen():
     torch.testing.assert_close(co, out, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(cls, ls, rtol=1e-5, atol=1e-6)
     dout = torch.randn_like(u)
+    co64, cls64 = c_oracle.fwd64(u, dl, A, Bm, Cm, Dv, z, b, True, cu_seqlens=cu)
+    h64 = scan_fwd64(_np(u), _np(dl), _np(A), _np(Bm), _np(Cm), _np(Dv), _np(z), _np(b), True,
+                     cu_seqlens=cu.numpy())
+    np.testing.assert_allclose(co64.numpy(), h64["out"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(cls64.numpy(), h64["last_state"], rtol=1e-12, atol=1e-12)
     cg = c_oracle.bwd(u, dl, A, Bm, Cm, dout, Dv, z, b, True, cu_seqlens=cu)
     h = scan_bwd64(_np(u), _np(dl), _np(A), _np(Bm), _np(Cm), _np(dout), _np(Dv), _np(z), _np(b),
                    True, cu_seqlens=cu.numpy())
