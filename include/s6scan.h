@@ -40,8 +40,9 @@
  * Errors: every entry point returns S6_OK (0) or a negative S6_E* code; the message of the
  * last failure on the calling thread is returned by s6_last_error().
  * Streams: all device work is enqueued on the given hipStream_t (NULL = default stream),
- * asynchronously; the library keeps no pointers after return and holds no global
- * device state, so calls on different streams with different workspaces may overlap.
+ * asynchronously; the library keeps no pointers after return and, apart from the scratch
+ * array of s6_fwd_noalloc, holds no global device state, so calls on different streams
+ * with different workspaces may overlap.
  */
 #ifndef S6SCAN_H
 #define S6SCAN_H
@@ -57,6 +58,7 @@ extern "C" {
 #define S6_CKPT_INTERVAL 8    /* steps between saved states in x_ckpt */
 #define S6_MAX_DSTATE_FWD 64
 #define S6_MAX_DSTATE_BWD 64
+#define S6_NOALLOC_SCRATCH_BYTES 67108864  /* scratch of s6_fwd_noalloc, per device (64 MiB) */
 
 enum s6_dtype { S6_F32 = 0, S6_BF16 = 1, S6_F16 = 2 };
 
@@ -162,6 +164,17 @@ size_t s6_bwd_workspace_bytes(const S6Problem* p);
 
 /* Forward scan: replaces selective_scan_cuda.fwd (selective_scan_interface.py:42). */
 int s6_fwd(const S6FwdArgs* a, void* stream);
+
+/* Forward scan that allocates nothing.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as s6_fwd, except
+ * that a->workspace / a->workspace_bytes are ignored: the workspace is a library-owned
+ * array of S6_NOALLOC_SCRATCH_BYTES on each device, kept until the process ends.  A problem
+ * whose workspace (s6_fwd_workspace_bytes) exceeds that returns S6_E_WORKSPACE before any
+ * device work.  The caller still allocates every input and output.  All calls on one
+ * device share its array: calls that overlap in time on one device (different streams, or
+ * threads) race and must be serialised by the caller.  Calls no hipMalloc / hipFree. */
+int s6_fwd_noalloc(const S6FwdArgs* a, void* stream);
 
 /* Backward scan: replaces selective_scan_cuda.bwd (selective_scan_interface.py:67-70).
  * dA, dB, dC, dD, ddelta_bias are overwritten (not accumulated into). */

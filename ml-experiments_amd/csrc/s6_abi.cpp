@@ -5,15 +5,59 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "s6_internal.h"
 #include "selective_state_update.h"
 #include "ssd.h"
 
+// Scratch of the no-allocation forward (s6_fwd_noalloc): one array per device, holding the
+// forward's workspace (chunk summaries, B/C relayout).  Every region of it that a forward
+// reads is written earlier in the same call, so nothing needs clearing between calls.  In
+// host code `scratch` names a host-side stand-in, not a device address: kernels and copies
+// get the address that hipGetSymbolAddress returns for each device (g_scratch_ptr below).
+static __device__ __align__(256) unsigned char scratch[S6_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_last_error;
+
+int validate_fwd(const S6FwdArgs* a, bool check_workspace);
+int run_fwd(const S6FwdArgs& a, hipStream_t st);
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int fail(int code, const char* fmt, ...);
+
+// Device address of this device's scratch array, looked up once per device with that
+// device current (the stream's device; the null stream means the current one).
+int scratch_for_stream(hipStream_t st, void** out) {
+  int dev = -1, cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess) e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_fwd_noalloc: cannot query the device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(S6_E_UNSUPPORTED, "s6_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(S6_E_HIP, "s6_fwd_noalloc: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(S6_E_HIP, "s6_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return S6_OK;
+}
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -826,7 +870,15 @@ size_t s6_bwd_workspace_bytes(const S6Problem* p) {
   return make_plan(*p, true, nullptr, nullptr, nullptr, nullptr).total_bwd;
 }
 
-int s6_validate_fwd(const S6FwdArgs* a) {
+int s6_validate_fwd(const S6FwdArgs* a) { return validate_fwd(a, true); }
+
+}  // extern "C"
+
+namespace {
+
+// Forward argument checks; the workspace size is checked unless the caller supplies the
+// workspace itself (the no-allocation entry point).
+int validate_fwd(const S6FwdArgs* a, bool check_workspace) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
   const S6Problem& p = a->p;
   int r = check_common(p, a->u, a->u_stride, a->delta, a->delta_stride, a->A, a->A_stride,
@@ -843,11 +895,16 @@ int s6_validate_fwd(const S6FwdArgs* a) {
       (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
       (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_z_stride, es, pl.Lc, "out_z")))))
     return r;
-  if (pl.total_fwd > 0 && (a->workspace == nullptr || a->workspace_bytes < pl.total_fwd))
+  if (check_workspace && pl.total_fwd > 0 &&
+      (a->workspace == nullptr || a->workspace_bytes < pl.total_fwd))
     return fail(S6_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", pl.total_fwd,
                 a->workspace ? a->workspace_bytes : (size_t)0);
   return ok();
 }
+
+}  // namespace
+
+extern "C" {
 
 int s6_validate_bwd(const S6BwdArgs* a) {
   if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
@@ -893,8 +950,35 @@ int s6_validate_bwd(const S6BwdArgs* a) {
 int s6_fwd(const S6FwdArgs* a, void* stream) {
   int r = s6_validate_fwd(a);
   if (r != S6_OK) return r;
+  return run_fwd(*a, (hipStream_t)stream);
+}
+
+// The forward with its workspace in the library's per-device scratch array.
+int s6_fwd_noalloc(const S6FwdArgs* a, void* stream) {
+  int r = validate_fwd(a, false);
+  if (r != S6_OK) return r;
+  const Plan pl = make_plan(a->p, false, a->B, a->B_stride, a->C, a->C_stride);
+  if (pl.total_fwd > (size_t)S6_NOALLOC_SCRATCH_BYTES)
+    return fail(S6_E_WORKSPACE,
+                "s6_fwd_noalloc: this problem needs %zu bytes of scratch, above the library's "
+                "fixed %d; call s6_fwd with a workspace instead",
+                pl.total_fwd, S6_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((r = scratch_for_stream((hipStream_t)stream, &ws)) != S6_OK) return r;
+  S6FwdArgs b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = S6_NOALLOC_SCRATCH_BYTES;
+  return run_fwd(b, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Launches of a validated forward.
+int run_fwd(const S6FwdArgs& args, hipStream_t st) {
+  const S6FwdArgs* a = &args;
   const S6Problem& p = a->p;
-  hipStream_t st = (hipStream_t)stream;
   const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
   char* ws = (char*)a->workspace;
   hipError_t e = hipSuccess;
@@ -913,6 +997,10 @@ int s6_fwd(const S6FwdArgs* a, void* stream) {
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_fwd: %s", hipGetErrorString(e));
   return ok();
 }
+
+}  // namespace
+
+extern "C" {
 
 int s6_bwd(const S6BwdArgs* a, void* stream) {
   int r = s6_validate_bwd(a);

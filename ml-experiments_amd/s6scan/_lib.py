@@ -19,6 +19,7 @@ ABI_VERSION = 6
 CKPT_INTERVAL = 8
 MAX_DSTATE_FWD = 64
 MAX_DSTATE_BWD = 64
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 F32, BF16, F16 = 0, 1, 2
 OK, E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_HIP = 0, -1, -2, -3, -4
@@ -211,6 +212,7 @@ EXPORTS = {
     "s6_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),
     "s6_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),
     "s6_fwd": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs), ctypes.c_void_p]),
+    "s6_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs), ctypes.c_void_p]),
     "s6_bwd": (ctypes.c_int, [ctypes.POINTER(S6BwdArgs), ctypes.c_void_p]),
     "s6_causal_conv1d_validate_fwd": (ctypes.c_int, [ctypes.POINTER(S6ConvFwdArgs)]),
     "s6_causal_conv1d_validate_bwd": (ctypes.c_int, [ctypes.POINTER(S6ConvBwdArgs)]),

@@ -182,14 +182,18 @@ def _ckpt_strides(x_ckpt):
 
 def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
                            delta_softplus=False, cu_seqlens=None, want_ckpt=True,
-                           want_last_state=False, kernel_events=None, x_ckpt_out=None):
+                           want_last_state=False, kernel_events=None, x_ckpt_out=None,
+                           no_alloc=False):
     """One forward launch.  Returns (out, out_z, x_ckpt, last_state); out_z is None without
     z, x_ckpt is None unless ``want_ckpt``, last_state is None unless ``want_last_state``.
     ``x_ckpt_out``: optional preallocated checkpoint view [batch, nck, dim, dstate] fp32 with
     a unit dstate stride and any other strides (nck = ceil(seqlen / 8)), written in place of
     a new contiguous one.
     ``kernel_events``: optional pair of already-recorded torch.cuda.Events that the library
-    re-records around its main scan kernel (measurement only)."""
+    re-records around its main scan kernel (measurement only).
+    ``no_alloc``: run ``s6_fwd_noalloc``, whose workspace is the library's per-device scratch
+    array, so the call allocates no device workspace (outputs are still new tensors unless
+    preallocated)."""
     dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
     batch, dim, seqlen, dstate, G, nseq = dims
     prob = _problem(u, B, z, D, delta_bias, delta_softplus, dims)
@@ -222,12 +226,17 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         args.out_z, args.out_z_stride = _ptr(out_z), _strides(out_z, 3)
         args.x_ckpt, args.x_ckpt_stride = _ptr(x_ckpt), _ckpt_strides(x_ckpt)
         args.last_state = _ptr(last_state)
-        nbytes = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob))
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=u.device)
-        args.workspace, args.workspace_bytes = _ptr(ws), nbytes
         args.kernel_events = _events(kernel_events)
         stream = torch.cuda.current_stream(u.device).cuda_stream
-        _lib.check(_lib.LIB.s6_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "s6_fwd")
+        if no_alloc:
+            args.workspace, args.workspace_bytes = None, 0
+            _lib.check(_lib.LIB.s6_fwd_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)),
+                       "s6_fwd_noalloc")
+        else:
+            nbytes = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(prob))
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=u.device)
+            args.workspace, args.workspace_bytes = _ptr(ws), nbytes
+            _lib.check(_lib.LIB.s6_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "s6_fwd")
     return out, out_z, x_ckpt, last_state
 
 

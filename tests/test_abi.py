@@ -253,3 +253,26 @@ def test_cu_seqlens_validator_accepts(values):
 
 def test_cu_seqlens_validator_null():
     assert _lib.LIB.s6_validate_cu_seqlens(None, 1, 100) == _lib.E_INVALID
+
+
+def test_noalloc_forward_rejects_problems_above_its_scratch():
+    """s6_fwd_noalloc checks the problem's workspace against its fixed per-device scratch on
+    the host and refuses before any device work (so this runs without a GPU; the pointers
+    are never dereferenced)."""
+    batch, dim, L, N = 64, 256, 65536, 16
+    p = _lib.S6Problem(batch, dim, L, N, 1, _lib.BF16, _lib.BF16, 1, 0, 0, 0, 0)
+    a = _lib.S6FwdArgs()
+    a.p = p
+    fake = ctypes.c_void_p(256)
+    a.u = a.delta = a.A = a.B = a.C = a.D = a.out = fake
+    a.u_stride = a.delta_stride = a.out_stride = (dim * L, L, 1)
+    a.A_stride = (N, 1)
+    a.B_stride = a.C_stride = (N * L, N * L, L, 1)      # L-contiguous rows: relaid out
+    a.D_stride = 1
+    need = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(p))
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    assert _lib.LIB.s6_fwd_noalloc(ctypes.byref(a), None) == _lib.E_WORKSPACE
+    assert "scratch" in _lib.last_error()
+    # argument errors are reported as by s6_fwd
+    a.u = None
+    assert _lib.LIB.s6_fwd_noalloc(ctypes.byref(a), None) == _lib.E_INVALID
