@@ -22,7 +22,7 @@ UNITS = [("s6_abi.cpp", "s6_abi", []), ("s6_misc.hip", "s6_misc", []),
          ("s6_conv.hip", "s6_conv", []), ("s6_ssu.hip", "s6_ssu", []),
          ("s6_ssd.hip", "s6_ssd", []), ("s6_ssd_bwd.hip", "s6_ssd_bwd", [])]
 UNITS += [(f"s6_{d}.hip", f"s6_{d}_{t}", [f"-DS6_TIO={ty}"])
-          for d in ("fwd", "bwd") for t, ty in _TIO.items()]
+          for d in ("fwd", "bwd", "fwd_lanes") for t, ty in _TIO.items()]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -3,6 +3,8 @@
 // they can be exercised (and are, by the CPU tests) on a machine without a GPU.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <mutex>
@@ -87,6 +89,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int esize(int dt) { return dt == S6_F32 ? 4 : 2; }
 
 struct Plan {
+  bool lanes;  // forward: single-pass kernel, one lane per (channel, state)
   int64_t Dg, nJ, nDblk;
   int64_t K, Lc, nck;
   bool relayout_B, relayout_C;
@@ -114,11 +117,52 @@ bool bc_scalar_ok(const void* ptr, const int64_t s[4], int dt, int64_t N, int64_
   return (s[0] % 2 == 0) && (s[1] % 2 == 0) && (s[3] % 2 == 0);
 }
 
+// Forward kernel choice.  The single-pass kernel (one lane per (channel, state), 16 / 32 / 64
+// lanes per channel) needs no chunk summaries, carries or B/C relayout, and does each
+// element's exp once, but it has only B * D * ceil16(N) / 64 waves and each one is a serial
+// chain.  Measured on the MI355X (same box, forward step time, chunked -> single-pass):
+//   B32 L4096 D256 N16 bf16 (2048 waves):               0.256 -> 0.232 ms
+//   B16 L16384 D256 N64 fp32 (4096 waves):              2.30  -> 1.76 ms
+//   B8 L8192 D768 N16 bf16, checkpoints (1536 waves):   forward slower (0.51 vs 0.28 +
+//                                                       summary pass)
+//   B32 L4096 D256 N16 bf16, softplus + z gate:         0.325 -> 0.367 ms
+// so it is used for dense batches with dstate 9-64, no z gate, and at least kLanesMinWaves
+// waves (two per SIMD).  S6_FWD_PATH=lanes or =chunked in the environment forces either one
+// (for measurement and tests); a forced single-pass choice still needs a dense batch and
+// dstate 9-64.
+constexpr int64_t kLanesMinWaves = 2048;
+
+int64_t lanes_ns(int64_t N) { return N <= 16 ? 16 : N <= 32 ? 32 : 64; }
+int64_t lanes_cpg(int64_t N) { return 4 * (64 / lanes_ns(N)); }  // channels per workgroup
+
+bool choose_lanes(const S6Problem& p) {
+  if (p.nseq > 0 || p.dstate < 9 || p.dstate > 64) return false;
+  const char* env = getenv("S6_FWD_PATH");
+  if (env != nullptr && strcmp(env, "chunked") == 0) return false;
+  if (env != nullptr && strcmp(env, "lanes") == 0) return true;
+  if (p.has_z) return false;
+  const int64_t Dg = p.dim / p.ngroups;
+  const int64_t waves = p.batch * p.ngroups * ceil_div(Dg, lanes_cpg(p.dstate)) * 4;
+  return waves >= kLanesMinWaves;
+}
+
 // Chunking and workspace layout; ptrs may be null (sizing only, then relayout is assumed
 // to be needed).
 Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, const void* Cp,
                const int64_t* sC) {
   Plan pl{};
+  if (!bwd && choose_lanes(p)) {
+    pl.lanes = true;
+    pl.Dg = p.dim / p.ngroups;
+    pl.nJ = ceil_div(pl.Dg, lanes_cpg(p.dstate));
+    pl.nDblk = p.ngroups * pl.nJ;
+    pl.Lc = p.seqlen;
+    pl.K = 1;
+    pl.nck = ceil_div(p.seqlen, s6::kCk);
+    pl.NP = lanes_ns(p.dstate);
+    pl.total_fwd = 0;  // no summaries, no relayout: B / C are read at any strides
+    return pl;
+  }
   pl.Dg = p.dim / p.ngroups;
   pl.nJ = ceil_div(pl.Dg, 64);
   pl.nDblk = p.ngroups * pl.nJ;
@@ -277,6 +321,7 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
   k.nDblk = pl.nDblk;
   k.nsg = (int32_t)nsg_fwd(p.dstate);
+  k.lanes = pl.lanes ? 1 : 0;
   return k;
 }
 
@@ -891,9 +936,11 @@ int validate_fwd(const S6FwdArgs* a, bool check_workspace) {
   if (a->x_ckpt != nullptr && (r = check_ckpt(a->x_ckpt_stride))) return r;
   const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
   const int es = esize(p.io_dtype);
-  if ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
-      (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
-      (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_z_stride, es, pl.Lc, "out_z")))))
+  // (the single-pass kernel addresses its tensors with 64-bit indices)
+  if (!pl.lanes &&
+      ((r = check_span(a->u_stride, es, pl.Lc, "u")) || (r = check_span(a->delta_stride, es, pl.Lc, "delta")) ||
+       (r = check_span(a->out_stride, es, pl.Lc, "out")) ||
+       (p.has_z && ((r = check_span(a->z_stride, es, pl.Lc, "z")) || (r = check_span(a->out_z_stride, es, pl.Lc, "out_z"))))))
     return r;
   if (check_workspace && pl.total_fwd > 0 &&
       (a->workspace == nullptr || a->workspace_bytes < pl.total_fwd))

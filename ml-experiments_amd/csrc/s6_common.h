@@ -264,8 +264,10 @@ struct FwdK {
   int32_t* ws_r;  // [Bsz*D, K]     1 if a sequence starts inside the chunk (varlen only)
   int64_t K, Lc;  // number of chunks and chunk length (multiple of kCk)
   int32_t has_D, has_z, has_bias, softplus;
-  int64_t nDblk;  // G * ceil(D / G / 64): 64-channel blocks per batch
+  int64_t nDblk;  // channel blocks per batch: G * ceil(D / G / 64) (chunked kernels) or
+                  // G * ceil(D / G / channels per workgroup) (single-pass kernel)
   int32_t nsg;    // dstate > 32: groups of 16 states, one wave each per workgroup (<= 4)
+  int32_t lanes;  // 1: single-pass kernel, one lane per (channel, state) (s6_fwd_lanes.hip)
 };
 
 }  // namespace s6

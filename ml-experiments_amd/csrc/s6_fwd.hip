@@ -325,6 +325,7 @@ static hipError_t launch_bc(const FwdK& k, hipStream_t st, void* const* ev) {
 
 template <typename Tio>
 hipError_t launch_fwd_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (k.lanes) return launch_fwd_lanes_io<Tio>(k, bc_dtype, st, ev);
   // B / C are either in the input dtype or fp32 (the interface enforces it).
   if (bc_dtype == S6_F32) return launch_bc<Tio, float>(k, st, ev);
   return launch_bc<Tio, Tio>(k, st, ev);

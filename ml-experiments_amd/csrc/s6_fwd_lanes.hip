@@ -1,0 +1,367 @@
+// Single-pass forward S6 selective scan for gfx950: one lane per (channel, state).
+//
+// The chunked forward (s6_fwd.hip) holds a channel's states in one lane and needs a second
+// pass over every chunk to obtain enough waves.  Here the 16 lanes of a DPP row each own one
+// state of the same channel (dstate 32 / 64: two / four rows per channel), so B * D * N / 64
+// waves run the whole sequence in one pass with no chunk summaries, no carry kernel and no
+// second exp per element.  Per 16-step block:
+//   * the block's u, delta (and z) of the wave's channels are loaded once, lane i of a row
+//     holding step sigma(i); Delta = prep(delta) and Delta u are formed there, and each step
+//     reads them back through a DPP row broadcast folded into its multiplies;
+//   * B_t and C_t of the block, shared by all channels of the workgroup (4 waves of the
+//     same batch and group), are staged in LDS as fp32 (B, C) pairs, double-buffered, one
+//     barrier per block;
+//   * each lane runs h = exp(Delta A) h + Delta u B on its state and keeps C h per step;
+//   * the 16 x 16 block of products of a row is reduced over the row's lanes with a DPP
+//     transpose-reduce (row mirror, half-row mirror, two quad exchanges), leaving lane i
+//     with y at step sigma(i), sigma(i) = i with bits 0 and 1 swapped; dstate 32 / 64 add
+//     the rows of a channel with lane shuffles;
+//   * lane i then applies D u and the z gate for step sigma(i) and stores it.
+// Checkpoints (the state after every S6_CKPT_INTERVAL-th step) and the final state are
+// stored by the state lanes, contiguous over (channel, state).  The recurrence and its
+// rounding points follow selective_scan_ref (selective_scan_interface.py:107-156), as the
+// chunked kernels do.  Dense batches only (no packed varlen); the dispatch in s6_abi.cpp
+// picks this kernel when B * D * N / 64 waves fill the chip.
+#include <type_traits>
+
+#include "s6_internal.h"
+
+namespace s6 {
+
+namespace {
+
+constexpr int kLT = 16;  // steps per block = lanes per row
+
+// row_newbcast:n -- every lane of a 16-lane row reads lane n of that row.
+template <int N>
+__device__ inline float bcast_lane(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x150 + N, 0xf, 0xf, true));
+}
+
+// f(std::integral_constant<int, I>{}) for I = 0 .. N-1, unrolled at compile time.
+template <int I, int N, typename F>
+__device__ inline void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+__device__ inline float dpp_row_mirror(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x140, 0xf, 0xf, true));
+}
+
+__device__ inline float dpp_half_mirror(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x141, 0xf, 0xf, true));
+}
+
+__device__ inline float dpp_qxor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0xB1, 0xf, 0xf, true));
+}
+
+__device__ inline float dpp_qxor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x4E, 0xf, 0xf, true));
+}
+
+// Sum over the 16 lanes of each row of pr[j] (lane = state, j = step).  Returns, on lane i,
+// the sum for step sigma(i).  i is the lane's index inside its row.
+__device__ inline float row_transpose_reduce16(const float (&pr)[kLT], int i) {
+  // lanes i and 15 - i: lanes 0-7 keep steps 0-7, lanes 8-15 steps 8-15
+  const bool hi8 = i >= 8;
+  float q[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float keep = hi8 ? pr[j + 8] : pr[j];
+    const float send = hi8 ? pr[j] : pr[j + 8];
+    q[j] = keep + dpp_row_mirror(send);
+  }
+  // lanes i and the mirror inside the half row: lanes with bit 2 clear keep q0-3
+  const bool b2 = (i & 4) != 0;
+  float r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float keep = b2 ? q[j + 4] : q[j];
+    const float send = b2 ? q[j] : q[j + 4];
+    r[j] = keep + dpp_half_mirror(send);
+  }
+  // quad exchange over bit 0: even lanes keep r0, r1
+  const bool b0 = (i & 1) != 0;
+  float s2[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b0 ? r[k + 2] : r[k];
+    const float send = b0 ? r[k] : r[k + 2];
+    s2[k] = keep + dpp_qxor1(send);
+  }
+  // quad exchange over bit 1
+  const bool b1 = (i & 2) != 0;
+  const float keep = b1 ? s2[1] : s2[0];
+  const float send = b1 ? s2[0] : s2[1];
+  return keep + dpp_qxor2(send);
+}
+
+// A lane offset chosen by a select, passed through an empty asm so that the compiler keeps
+// the select (one v_cndmask) instead of splitting the access into two masked branches.
+__device__ inline uint32_t pick_off(bool drop, uint32_t off) {
+  uint32_t v = drop ? kOffDrop : off;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+constexpr int sigma(int i) { return (i & ~3) | ((i & 1) << 1) | ((i & 2) >> 1); }
+
+// Raw buffer loads kept as bits until first use: a prefetched value carried across a loop
+// iteration must not be converted right after its load, or the conversion waits for it.
+template <typename T> struct Raw;
+template <> struct Raw<float> {
+  __device__ static inline uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, 0, 0);
+  }
+  __device__ static inline float get(uint32_t x) { return __uint_as_float(x); }
+};
+template <> struct Raw<bf16> {
+  __device__ static inline uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, 0, 0);
+  }
+  __device__ static inline float get(uint32_t x) { return __uint_as_float(x << 16); }
+};
+template <> struct Raw<f16> {
+  __device__ static inline uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, 0, 0);
+  }
+  __device__ static inline float get(uint32_t x) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
+  }
+};
+
+}  // namespace
+
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+__global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
+  constexpr int RPC = NS / 16;        // rows (of 16 lanes) per channel
+  constexpr int CPW = 4 / RPC;        // channels per wave
+  constexpr int CPG = 4 * CPW;        // channels per workgroup
+  constexpr int NBC = kLT * NS / 256; // B/C elements staged per thread per block
+  constexpr int ES = Elem<Tio>::kSize, EB = Elem<Tbc>::kSize;
+  __shared__ float2 bcs[2][kLT][NS];
+
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, row = lane >> 4, li = lane & 15;
+  const int sg = sigma(li);
+  const BlockPos bp = block_pos(p.Bsz * p.nDblk);
+  const int64_t Dg = p.D / p.G;
+  const int64_t nJ = p.nDblk / p.G;
+  const int64_t b = bp.x / p.nDblk;
+  const int64_t rem = bp.x % p.nDblk;
+  const int64_t g = rem / nJ;
+  const int64_t jb = rem % nJ;
+  const int cr = row / RPC;                    // channel of this lane within its wave
+  const int s = (row % RPC) * 16 + li;         // state of this lane
+  const int64_t dl0 = jb * CPG + w * CPW;      // first channel of the wave, within the group
+  const bool active = dl0 + cr < Dg;
+  // inactive lanes (past the group's last channel) mirror its last channel and store nothing
+  const int cre = active ? cr : (int)(Dg - 1 - dl0);
+  const int64_t d0 = g * Dg + dl0;             // wave-uniform
+  const int64_t d = d0 + cre;
+  const int N = (int)p.N;
+  const bool live = s < N;
+  const int L = (int)p.L;
+
+  const float Ap = live ? p.A[d * p.sA[0] + s * p.sA[1]] * kLog2e : 0.f;
+  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
+  const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
+
+  // Buffer addressing (s6_common.h): a wave-uniform base rebuilt per block and 32-bit lane
+  // offsets; lanes given kOffDrop read zeros and drop their stores, so no store needs a
+  // divergent branch inside the block.
+  const char* const ub = (const char*)p.u + (b * p.su[0] + d0 * p.su[1]) * ES;
+  const char* const db = (const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1]) * ES;
+  const char* const zb = HAS_Z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1]) * ES : ub;
+  char* const ob = (char*)p.out + (b * p.so[0] + d0 * p.so[1]) * ES;
+  char* const ozb = HAS_Z ? (char*)p.out_z + (b * p.soz[0] + d0 * p.soz[1]) * ES : ob;
+  const uint32_t vu = (uint32_t)((cre * p.su[1] + sg * p.su[2]) * ES);
+  const uint32_t vd = (uint32_t)((cre * p.sdl[1] + sg * p.sdl[2]) * ES);
+  const uint32_t vz = HAS_Z ? (uint32_t)((cre * p.sz[1] + sg * p.sz[2]) * ES) : 0u;
+  const bool store_y = active && (row % RPC) == 0;
+  const uint32_t vo = store_y ? (uint32_t)((cr * p.so[1] + sg * p.so[2]) * ES) : kOffDrop;
+  const uint32_t voz = (HAS_Z && store_y) ? (uint32_t)((cr * p.soz[1] + sg * p.soz[2]) * ES) : kOffDrop;
+  const bool store_state = active && live;
+  float* const xb = p.x_ckpt != nullptr ? p.x_ckpt + b * p.sck[0] + d0 * p.sck[2] : nullptr;
+  const uint32_t vck = store_state ? (uint32_t)((cr * p.sck[2] + s) * 4) : kOffDrop;
+
+  // B / C staging: element e = tid + 256 m of the block's [kLT][NS] tile.
+  const char* const Bb = (const char*)p.Bm + (b * p.sB[0] + g * p.sB[1]) * EB;
+  const char* const Cb = (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1]) * EB;
+  uint32_t vb[NBC], vc[NBC];
+  int btt[NBC];
+#pragma unroll
+  for (int m = 0; m < NBC; ++m) {
+    const int e = tid + 256 * m;
+    const int tt = e / NS, sn = e % NS;
+    btt[m] = tt;
+    vb[m] = sn < N ? (uint32_t)((sn * p.sB[2] + tt * p.sB[3]) * EB) : kOffDrop;
+    vc[m] = sn < N ? (uint32_t)((sn * p.sC[2] + tt * p.sC[3]) * EB) : kOffDrop;
+  }
+  // Inputs of one block, loaded two blocks ahead of use: the B / C tile (committed to LDS
+  // at the end of the block before its own) and this lane's u / delta / z.
+  struct Pref {
+    uint32_t b[NBC], c[NBC];
+    uint32_t u, dl, z;
+  };
+  auto issue = [&](Pref& P, int t0) {
+    const auto rb = make_rsrc(Bb + (int64_t)t0 * p.sB[3] * EB);
+    const auto rc = make_rsrc(Cb + (int64_t)t0 * p.sC[3] * EB);
+    const bool tail = t0 + kLT > L;  // wave-uniform; rows past the end read zeros
+#pragma unroll
+    for (int m = 0; m < NBC; ++m) {
+      const bool out = tail && t0 + btt[m] >= L;
+      P.b[m] = Raw<Tbc>::load(rb, pick_off(out, vb[m]));
+      P.c[m] = Raw<Tbc>::load(rc, pick_off(out, vc[m]));
+    }
+    const bool out = tail && t0 + sg >= L;
+    P.u = Raw<Tio>::load(make_rsrc(ub + (int64_t)t0 * p.su[2] * ES), pick_off(out, vu));
+    P.dl = Raw<Tio>::load(make_rsrc(db + (int64_t)t0 * p.sdl[2] * ES), pick_off(out, vd));
+    P.z = HAS_Z ? Raw<Tio>::load(make_rsrc(zb + (int64_t)t0 * p.sz[2] * ES), pick_off(out, vz))
+                : 0u;
+  };
+  auto commit = [&](const Pref& P, int buf) {
+#pragma unroll
+    for (int m = 0; m < NBC; ++m) {
+      const int e = tid + 256 * m;
+      bcs[buf][e / NS][e % NS] = make_float2(Raw<Tbc>::get(P.b[m]), Raw<Tbc>::get(P.c[m]));
+    }
+  };
+
+  // Checkpoint rows: without a checkpoint tensor the resource holds no records, so its
+  // stores are dropped (no branch in the block).
+  float* const ck_base = xb != nullptr ? xb : (float*)ob;
+  const int ck_records = xb != nullptr ? (int)kBufRecords : 0;
+  const uint32_t ck_step = (uint32_t)(p.sck[1] * 4);
+
+  Pref P0, P1;  // inputs of even / odd blocks
+  issue(P0, 0);
+  issue(P1, kLT);
+  commit(P0, 0);
+  __syncthreads();
+
+  float h = 0.f;
+  // One block of kLT steps from t0 (block index parity PAR: its inputs are in P0 / P1 and
+  // its B / C tile in LDS buffer PAR).  FULL: t0 + kLT <= L (no per-step bounds).  The body
+  // holds no branch, so the DPP row broadcasts fold into the multiplies that use them.
+  auto block = [&](int t0, auto full_tag, auto par_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    constexpr int PAR = decltype(par_tag)::value;
+    Pref& Pc = PAR == 0 ? P0 : P1;  // this block's inputs; reloaded for block + 2 below
+    Pref& Pn = PAR == 0 ? P1 : P0;  // the next block's (B / C committed at the end)
+    const float uu = Raw<Tio>::get(Pc.u), zz = HAS_Z ? Raw<Tio>::get(Pc.z) : 0.f;
+    const float dt = prep_dt<DTM>(Raw<Tio>::get(Pc.dl), bias);
+    const float dtu = dt * uu;
+    issue(Pc, t0 + 2 * kLT);
+    // Phase 1: the block's B / C pairs from LDS, then everything that does not depend on
+    // the state -- exp(Delta A) and Delta u B of all kLT steps -- so that the LDS and
+    // transcendental latencies overlap instead of sitting on the recurrence.
+    float2 bc[kLT];
+    static_for<0, kLT>([&](auto J) { bc[decltype(J)::value] = bcs[PAR][decltype(J)::value][s]; });
+    float a[kLT], bx[kLT];
+    static_for<0, kLT>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      a[j] = fast_exp2(bcast_lane<sigma(j)>(dt) * Ap);
+    });
+    static_for<0, kLT>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      bx[j] = bcast_lane<sigma(j)>(dtu) * bc[j].x;
+    });
+    // Phase 2: the recurrence, one dependent FMA per step; checkpoints after every kCk-th
+    // step and after the last one.
+    const auto rck = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(ck_base + (int64_t)(t0 / kCk) * p.sck[1]), (short)0, ck_records, 0x00020000);
+    float pr[kLT];
+    static_for<0, kLT>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int t = t0 + j;
+      if (!FULL && t >= L) {
+        pr[j] = 0.f;
+        return;
+      }
+      h = fmaf(a[j], h, bx[j]);
+      pr[j] = bc[j].y * h;
+      constexpr bool at_ck = (j & (kCk - 1)) == kCk - 1;
+      if (FULL ? at_ck : (at_ck || t == L - 1))
+        Buf<float>::store(rck, vck, (uint32_t)(j / kCk) * ck_step, h);
+    });
+    // Phase 3: y of step sigma(li), D u, gate, store.
+    float y = row_transpose_reduce16(pr, li);
+    if constexpr (RPC >= 2) y += __shfl_xor(y, 16);
+    if constexpr (RPC >= 4) y += __shfl_xor(y, 32);
+    const bool yout = !FULL && t0 + sg >= L;
+    y = fmaf(uu, Dv, y);
+    Buf<Tio>::store(make_rsrc(ob + (int64_t)t0 * p.so[2] * ES), FULL ? vo : pick_off(yout, vo), 0, y);
+    if (HAS_Z)
+      Buf<Tio>::store(make_rsrc(ozb + (int64_t)t0 * p.soz[2] * ES), FULL ? voz : pick_off(yout, voz),
+                      0, y * zz * sigmoidf_(zz));
+    commit(Pn, PAR ^ 1);
+    __syncthreads();
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using P0_ = std::integral_constant<int, 0>;
+  using P1_ = std::integral_constant<int, 1>;
+  int t0 = 0;
+  for (; t0 + 2 * kLT <= L; t0 += 2 * kLT) {
+    block(t0, T_{}, P0_{});
+    block(t0 + kLT, T_{}, P1_{});
+  }
+  if (t0 + kLT <= L) {
+    block(t0, T_{}, P0_{});
+    t0 += kLT;
+    if (t0 < L) block(t0, F_{}, P1_{});
+  } else if (t0 < L) {
+    block(t0, F_{}, P0_{});
+  }
+  if (p.last_state != nullptr && store_state) p.last_state[(b * p.D + d) * p.N + s] = h;
+}
+
+template <typename Tio, typename Tbc, int NS, int DTM>
+static hipError_t launch_lanes_z(const FwdK& k, hipStream_t st, void* const* ev) {
+  hipError_t e = record_event(ev, 0, st);
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)(k.Bsz * k.nDblk));
+  if (k.has_z)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, true>), grid, dim3(256), 0, st, k);
+  else
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false>), grid, dim3(256), 0, st, k);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return record_event(ev, 1, st);
+}
+
+template <typename Tio, typename Tbc, int NS>
+static hipError_t launch_lanes_dt(const FwdK& k, hipStream_t st, void* const* ev) {
+  switch (dt_mode(k.has_bias, k.softplus)) {
+    case kDtRaw: return launch_lanes_z<Tio, Tbc, NS, kDtRaw>(k, st, ev);
+    case kDtBias: return launch_lanes_z<Tio, Tbc, NS, kDtBias>(k, st, ev);
+    default: return launch_lanes_z<Tio, Tbc, NS, kDtSoftplus>(k, st, ev);
+  }
+}
+
+template <typename Tio, typename Tbc>
+static hipError_t launch_lanes_ns(const FwdK& k, hipStream_t st, void* const* ev) {
+  if (k.N <= 16) return launch_lanes_dt<Tio, Tbc, 16>(k, st, ev);
+  if (k.N <= 32) return launch_lanes_dt<Tio, Tbc, 32>(k, st, ev);
+  return launch_lanes_dt<Tio, Tbc, 64>(k, st, ev);
+}
+
+template <typename Tio>
+hipError_t launch_fwd_lanes_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (bc_dtype == S6_F32) return launch_lanes_ns<Tio, float>(k, st, ev);
+  return launch_lanes_ns<Tio, Tio>(k, st, ev);
+}
+
+template hipError_t launch_fwd_lanes_io<S6_TIO>(const FwdK&, int, hipStream_t, void* const*);
+
+}  // namespace s6

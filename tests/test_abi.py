@@ -259,7 +259,7 @@ def test_noalloc_forward_rejects_problems_above_its_scratch():
     """s6_fwd_noalloc checks the problem's workspace against its fixed per-device scratch on
     the host and refuses before any device work (so this runs without a GPU; the pointers
     are never dereferenced)."""
-    batch, dim, L, N = 64, 256, 65536, 16
+    batch, dim, L, N = 64, 256, 65536, 8      # dstate 8: the chunked forward (workspace)
     p = _lib.S6Problem(batch, dim, L, N, 1, _lib.BF16, _lib.BF16, 1, 0, 0, 0, 0)
     a = _lib.S6FwdArgs()
     a.p = p

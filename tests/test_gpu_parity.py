@@ -304,7 +304,10 @@ def test_state_groups_forward(N, z, varlen, dtype):
     _grads_vs_ref(inp, cu)
 
 
-def test_varlen_equals_independent_sequences_on_gpu():
+def test_varlen_equals_independent_sequences_on_gpu(monkeypatch):
+    # bit-for-bit equality holds within one kernel family: packed varlen always runs the
+    # chunked forward, so the separate per-sequence calls are pinned to it too
+    monkeypatch.setenv("S6_FWD_PATH", "chunked")
     inp = gen(1, 3000, 128, 16, torch.bfloat16, seed=12)
     cu = torch.tensor([0, 700, 701, 1900, 3000], dtype=torch.int32)
     args, kw = call(inp, "view", DEV)

@@ -120,3 +120,28 @@ def test_cfg2_kernel_no_farther_from_exact_than_fp32_restatement():
                 f"the fp32 restatement + bar; worst: kernel {k.flatten()[j].item():.9g}, ref32 "
                 f"{r.flatten()[j].item():.9g}, f64 {e.flatten()[j].item():.12g}")
     print("\n".join(report))
+
+
+@pytest.mark.parametrize("path", ["lanes", "chunked"])
+def test_bias_mode_fp32_no_farther_from_exact_than_reference_order(path, monkeypatch):
+    """The bias-only delta mode in fp32 (large steps, strongly cancelling outputs, with the z
+    gate) on both forward kernels.  The single-pass kernel rounds each C h product before
+    its tree sum, as the reference's fp32 order does (selective_scan_interface.py:144: x * C,
+    then the sum), so at cancelling outputs it lands about as far from the float64 value as
+    the reference itself.  Every output and final state satisfies
+        |kernel - f64| <= |ref32 - f64| + 1e-6 + 1e-5 |f64|."""
+    from test_gpu_parity import call, gen
+
+    monkeypatch.setenv("S6_FWD_PATH", path)
+    inp = gen(2, 1203, 96, 16, torch.float32, seed=17, z=True, bias=True, softplus=False)
+    args, kw = call(inp, "view", DEV)
+    out, ls = s6scan.selective_scan_fn(*args, **kw)
+    cargs, ckw = call(inp, "view", "cpu")
+    okw = dict(D=ckw["D"], z=ckw["z"], delta_bias=ckw["delta_bias"], delta_softplus=False)
+    r32, rls32 = c_oracle.fwd(*cargs, **okw)
+    r64, rls64 = c_oracle.fwd64(*cargs, **okw)
+    for what, k, r, e in (("y", out.cpu(), r32, r64), ("last_state", ls.cpu(), rls32, rls64)):
+        ek = (k.double() - e).abs()
+        er = (r.double() - e).abs()
+        bad = ek > er + 1e-6 + 1e-5 * e.abs()
+        assert not bad.any(), f"{path} {what}: {int(bad.sum())} elements; max |k-f64| {ek.max():.3g}"

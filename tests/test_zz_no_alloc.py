@@ -24,7 +24,10 @@ def _run(i, no_alloc, z=None, bias=None, softplus=False, cu=None):
     return [t for t in (out, out_z, ck, ls) if t is not None]
 
 
-def test_noalloc_forward_equals_workspace_forward_twice():
+def test_noalloc_forward_equals_workspace_forward_twice(monkeypatch):
+    # the chunked forward is the one with a workspace (chunk summaries): force it for the
+    # dense problem, which the library would otherwise run on its single-pass kernel
+    monkeypatch.setenv("S6_FWD_PATH", "chunked")
     print("case: cfg1 shape (workspace ~18 MB), then a smaller varlen problem with z", flush=True)
     big = {k: v.to(DEV) for k, v in make_inputs(CONFIGS[1]).items()}
     need = _lib.LIB.s6_fwd_workspace_bytes(ctypes.byref(s6scan.selective_scan_interface._problem(
@@ -46,5 +49,12 @@ def test_noalloc_forward_equals_workspace_forward_twice():
     ref = _run(small, False, **kw)
     got = _run(small, True, **kw)
     assert len(got) == 4
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    # and with a problem the single-pass kernel runs (no workspace at all)
+    monkeypatch.setenv("S6_FWD_PATH", "lanes")
+    ref = _run(small3 := {k: v[:, :512] if k in ("x", "delta", "B", "C") else v
+                          for k, v in small.items() if k != "cu_seqlens"}, False)
+    got = _run(small3, True)
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
