@@ -31,6 +31,11 @@ namespace s6 {
 namespace {
 
 constexpr int kLT = 16;  // steps per block = lanes per row
+// Blocks between the load of a block's inputs and their use (even): 4 hides HBM latency at 2
+// waves per SIMD (B32 L4096 D256 N16: kernel 236 -> 224 us); at 64 states the extra
+// registers cost the kernel its 4 waves per SIMD (B16 L16384 D256 N64: 1.75 -> 1.85 ms with
+// 4), so it keeps 2.
+template <int NS> constexpr int kPD = NS <= 32 ? 4 : 2;
 
 // row_newbcast:n -- every lane of a 16-lane row reads lane n of that row.
 template <int N>
@@ -48,16 +53,6 @@ __device__ inline void static_for(F&& f) {
   }
 }
 
-__device__ inline float dpp_row_mirror(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x140, 0xf, 0xf, true));
-}
-
-__device__ inline float dpp_half_mirror(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x141, 0xf, 0xf, true));
-}
-
 __device__ inline float dpp_qxor1(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
                                                                0xB1, 0xf, 0xf, true));
@@ -68,27 +63,36 @@ __device__ inline float dpp_qxor2(float v) {
                                                                0x4E, 0xf, 0xf, true));
 }
 
+// Bank-masked DPP adds (a bank is 4 consecutive lanes of a row).  out = x[perm] + x on the
+// lanes of banks `MLO` and y[perm] + y on those of `MHI`, perm = row_mirror (lane i <-> 15 - i)
+// or row_half_mirror (i <-> 7 - i inside each half row): two VALU instructions where a
+// select-based exchange takes three.  Inline asm because the write masks must not be
+// merged away; the s_nop covers the VALU-write -> DPP-read distance for x and y.
+#define S6_MASKED_PAIR(CTRL, MLO, MHI)                                                    \
+  __device__ inline float masked_pair_##CTRL(float x, float y) {                          \
+    float out;                                                                            \
+    asm("s_nop 1\n\t"                                                                   \
+        "v_add_f32_dpp %0, %1, %1 " #CTRL " row_mask:0xf bank_mask:" #MLO "\n\t"         \
+        "v_add_f32_dpp %0, %2, %2 " #CTRL " row_mask:0xf bank_mask:" #MHI                 \
+        : "=&v"(out)                                                                      \
+        : "v"(x), "v"(y));                                                                \
+    return out;                                                                           \
+  }
+S6_MASKED_PAIR(row_mirror, 0x3, 0xc)
+S6_MASKED_PAIR(row_half_mirror, 0x5, 0xa)
+#undef S6_MASKED_PAIR
+
 // Sum over the 16 lanes of each row of pr[j] (lane = state, j = step).  Returns, on lane i,
 // the sum for step sigma(i).  i is the lane's index inside its row.
 __device__ inline float row_transpose_reduce16(const float (&pr)[kLT], int i) {
-  // lanes i and 15 - i: lanes 0-7 keep steps 0-7, lanes 8-15 steps 8-15
-  const bool hi8 = i >= 8;
+  // lanes i and 15 - i: lanes 0-7 (banks 0, 1) keep steps 0-7, lanes 8-15 steps 8-15
   float q[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float keep = hi8 ? pr[j + 8] : pr[j];
-    const float send = hi8 ? pr[j] : pr[j + 8];
-    q[j] = keep + dpp_row_mirror(send);
-  }
-  // lanes i and the mirror inside the half row: lanes with bit 2 clear keep q0-3
-  const bool b2 = (i & 4) != 0;
+  for (int j = 0; j < 8; ++j) q[j] = masked_pair_row_mirror(pr[j], pr[j + 8]);
+  // lanes i and 7 - i of each half row: banks 0 and 2 keep q0-3, banks 1 and 3 q4-7
   float r[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float keep = b2 ? q[j + 4] : q[j];
-    const float send = b2 ? q[j] : q[j + 4];
-    r[j] = keep + dpp_half_mirror(send);
-  }
+  for (int j = 0; j < 4; ++j) r[j] = masked_pair_row_half_mirror(q[j], q[j + 4]);
   // quad exchange over bit 0: even lanes keep r0, r1
   const bool b0 = (i & 1) != 0;
   float s2[2];
@@ -144,6 +148,7 @@ template <> struct Raw<f16> {
 template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
 __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   constexpr int RPC = NS / 16;        // rows (of 16 lanes) per channel
+  constexpr int PD = kPD<NS>;         // prefetch distance in blocks
   constexpr int CPW = 4 / RPC;        // channels per wave
   constexpr int CPG = 4 * CPW;        // channels per workgroup
   constexpr int NBC = kLT * NS / 256; // B/C elements staged per thread per block
@@ -244,30 +249,32 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   const int ck_records = xb != nullptr ? (int)kBufRecords : 0;
   const uint32_t ck_step = (uint32_t)(p.sck[1] * 4);
 
-  Pref P0, P1;  // inputs of even / odd blocks
-  issue(P0, 0);
-  issue(P1, kLT);
-  commit(P0, 0);
+  // Inputs are loaded PD blocks ahead of use (block k's in P[k % PD]); the B / C tiles
+  // are double-buffered in LDS (block k's in buffer k % 2).
+  Pref P[PD];
+  static_for<0, PD>([&](auto Q) { issue(P[decltype(Q)::value], decltype(Q)::value * kLT); });
+  commit(P[0], 0);
   __syncthreads();
 
   float h = 0.f;
-  // One block of kLT steps from t0 (block index parity PAR: its inputs are in P0 / P1 and
-  // its B / C tile in LDS buffer PAR).  FULL: t0 + kLT <= L (no per-step bounds).  The body
-  // holds no branch, so the DPP row broadcasts fold into the multiplies that use them.
+  // One block of kLT steps from t0 (block index mod PD = PAR).  FULL: t0 + kLT <= L (no
+  // per-step bounds).  The body holds no branch, so the DPP row broadcasts fold into the
+  // multiplies that use them.
   auto block = [&](int t0, auto full_tag, auto par_tag) {
     constexpr bool FULL = decltype(full_tag)::value;
     constexpr int PAR = decltype(par_tag)::value;
-    Pref& Pc = PAR == 0 ? P0 : P1;  // this block's inputs; reloaded for block + 2 below
-    Pref& Pn = PAR == 0 ? P1 : P0;  // the next block's (B / C committed at the end)
+    constexpr int BUF = PAR & 1;
+    Pref& Pc = P[PAR];           // this block's inputs; reloaded for block + PD below
+    Pref& Pn = P[(PAR + 1) % PD];  // the next block's (B / C committed at the end)
     const float uu = Raw<Tio>::get(Pc.u), zz = HAS_Z ? Raw<Tio>::get(Pc.z) : 0.f;
     const float dt = prep_dt<DTM>(Raw<Tio>::get(Pc.dl), bias);
     const float dtu = dt * uu;
-    issue(Pc, t0 + 2 * kLT);
+    issue(Pc, t0 + PD * kLT);
     // Phase 1: the block's B / C pairs from LDS, then everything that does not depend on
     // the state -- exp(Delta A) and Delta u B of all kLT steps -- so that the LDS and
     // transcendental latencies overlap instead of sitting on the recurrence.
     float2 bc[kLT];
-    static_for<0, kLT>([&](auto J) { bc[decltype(J)::value] = bcs[PAR][decltype(J)::value][s]; });
+    static_for<0, kLT>([&](auto J) { bc[decltype(J)::value] = bcs[BUF][decltype(J)::value][s]; });
     float a[kLT], bx[kLT];
     static_for<0, kLT>([&](auto J) {
       constexpr int j = decltype(J)::value;
@@ -305,25 +312,24 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
     if (HAS_Z)
       Buf<Tio>::store(make_rsrc(ozb + (int64_t)t0 * p.soz[2] * ES), FULL ? voz : pick_off(yout, voz),
                       0, y * zz * sigmoidf_(zz));
-    commit(Pn, PAR ^ 1);
+    commit(Pn, BUF ^ 1);
     __syncthreads();
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  using P0_ = std::integral_constant<int, 0>;
-  using P1_ = std::integral_constant<int, 1>;
   int t0 = 0;
-  for (; t0 + 2 * kLT <= L; t0 += 2 * kLT) {
-    block(t0, T_{}, P0_{});
-    block(t0 + kLT, T_{}, P1_{});
-  }
-  if (t0 + kLT <= L) {
-    block(t0, T_{}, P0_{});
-    t0 += kLT;
-    if (t0 < L) block(t0, F_{}, P1_{});
-  } else if (t0 < L) {
-    block(t0, F_{}, P0_{});
-  }
+  for (; t0 + PD * kLT <= L; t0 += PD * kLT)
+    static_for<0, PD>([&](auto Q) { block(t0 + decltype(Q)::value * kLT, T_{}, Q); });
+  // up to PD - 1 remaining full blocks and the partial one, in block order
+  static_for<0, PD>([&](auto Q) {
+    if (t0 + kLT <= L) {
+      block(t0, T_{}, Q);
+      t0 += kLT;
+    } else if (t0 < L) {
+      block(t0, F_{}, Q);
+      t0 = L;
+    }
+  });
   if (p.last_state != nullptr && store_state) p.last_state[(b * p.D + d) * p.N + s] = h;
 }
 
