@@ -98,18 +98,20 @@ def cpu_config0_one_thread(make_inputs):
             "threads": 1}
 
 
-def cpu_baseline(cfg, make_inputs, mixer=False):
+def cpu_baseline(cfg, make_inputs, mixer=False, one_thread=True, seqlen=None):
     """Reference CPU path on a bounded sample: one sequence of the workload (4096 steps
-    forward, 2048 steps forward + backward).  The scan workloads time the torch restatement
-    of selective_scan_ref (op for op); the mixer workload the restatement of the reference
-    SSMMixer's own scan loop (backbone.py:1207-1242, state in the input dtype as there)."""
+    forward, 2048 steps forward + backward, or ``seqlen``).  The scan workloads time the torch
+    restatement of selective_scan_ref (op for op); the mixer workload the restatement of the
+    reference SSMMixer's own scan loop (backbone.py:1207-1242, state in the input dtype as
+    there)."""
     import dataclasses
 
     import torch
     from oracle.selective_scan_ref import selective_scan_ref, selective_scan_ref_grads
     from oracle.ssm_mixer_ref import ssm_mixer_scan_ref
     torch.set_num_threads(os.cpu_count() or 1)
-    seqlen = 2048 if (cfg.backward or not cfg.seqlen) else min(cfg.seqlen, 4096)
+    if seqlen is None:
+        seqlen = 2048 if (cfg.backward or not cfg.seqlen) else min(cfg.seqlen, 4096)
     sample = dataclasses.replace(cfg, batch=1, seqlen=seqlen, nseq=0)
     inp = make_inputs(sample)
     args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
@@ -143,7 +145,7 @@ def cpu_baseline(cfg, make_inputs, mixer=False):
                    f"median of 3 runs = {sec:.3f} s; os.cpu_count() = {os.cpu_count()}"),
         "mtok_ch_per_s": round(seqlen * cfg.dim / sec / 1e6, 4),
         "cpu_model": cpu_model(),
-        "config0_one_thread": cpu_config0_one_thread(make_inputs),
+        **({"config0_one_thread": cpu_config0_one_thread(make_inputs)} if one_thread else {}),
     }
 
 
@@ -370,7 +372,11 @@ def run_decode(torch, args):
         "roofline": {"kernel": "ssu_rows_kernel (one per step, graph-launched)", "bound": "hbm",
                      "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
-                     "kernel_us_incl_graph_gaps": round(ev_us, 3)},
+                     "kernel_us_incl_graph_gaps": round(ev_us, 3),
+                     "cache_resident": True,
+                     "note": (f"the {B * D * N * 4 / 1e6:.1f} MB fp32 state stays in the 256 MB "
+                              "Infinity Cache across the graph-replayed steps, so this rate is "
+                              "cache bandwidth plus launch gaps, not HBM bandwidth")},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -544,6 +550,9 @@ def copy_reference(torch, steps):
 def measure_scan(torch, workload, steps, warmup):
     """One of the scan workloads (fwd1, fwdbwd3, fwd2, fwdbwd4, mixer1): its bench dict,
     without the CPU baseline."""
+    import ctypes
+
+    from s6scan import _lib
     from s6scan.configs import CONFIGS, make_inputs
     from s6scan.selective_scan_interface import selective_scan_backward, selective_scan_forward
 
@@ -570,7 +579,7 @@ def measure_scan(torch, workload, steps, warmup):
     if mixer:  # + z read, + the gated output written next to the pre-gate one
         nbytes += 2 * B * L * cfg.dim * sets[0]["x"].element_size()
 
-    def step(i, ev=None, ev_b=None):
+    def step(i, ev=None, ev_b=None, ev_f=None):
         g = sets[i % nsets]
         a = (g["x"].mT, g["delta"].mT, g["A"], g["B"].mT, g["C"].mT)
         cu = g.get("cu_seqlens")
@@ -584,8 +593,12 @@ def measure_scan(torch, workload, steps, warmup):
                 selective_scan_forward(*a, D=g["D"], cu_seqlens=cu, want_ckpt=False,
                                        want_last_state=True, kernel_events=ev)
         else:
+            if ev_f is not None:
+                ev_f[0].record()
             out, _, xck, _ = selective_scan_forward(*a, D=g["D"], cu_seqlens=cu, want_ckpt=True,
                                                     want_last_state=True, kernel_events=ev)
+            if ev_f is not None:
+                ev_f[1].record()
             selective_scan_backward(*a, g["D"], None, None, False, g["dy"].mT, xck, cu_seqlens=cu,
                                     kernel_events=ev_b)
 
@@ -597,6 +610,7 @@ def measure_scan(torch, workload, steps, warmup):
     mk = lambda: torch.cuda.Event(enable_timing=True)
     evs = [(mk(), mk()) for _ in range(K)]
     evs_b = [(mk(), mk()) for _ in range(K)] if cfg.backward else [None] * K
+    evs_f = [(mk(), mk()) for _ in range(K)] if cfg.backward else [None] * K
     stream = torch.cuda.current_stream()
     for pair in evs + [p for p in evs_b if p is not None]:
         for e in pair:
@@ -606,7 +620,7 @@ def measure_scan(torch, workload, steps, warmup):
     t_start = time.perf_counter()
     g0.record(stream)
     for i in range(K):
-        step(i, evs[i], evs_b[i])
+        step(i, evs[i], evs_b[i], evs_f[i])
     g1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
@@ -614,26 +628,44 @@ def measure_scan(torch, workload, steps, warmup):
     gpu_ms_step = g0.elapsed_time(g1) / K
     k_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
     kb_ms = statistics.mean(a.elapsed_time(b) for a, b in evs_b) if cfg.backward else None
+    # whole forward (every kernel of the forward call): the step itself for the forward-only
+    # workloads, the events around the forward call for the fwd+bwd ones
+    fwd_ms = (statistics.mean(a.elapsed_time(b) for a, b in evs_f) if cfg.backward
+              else gpu_ms_step)
 
     value = nbytes / (ms_step * 1e-3) / 1e9
     fwd_bytes = cfg.algorithmic_bytes(seqlen=L, with_backward=False)
     # Dominant kernel: the scan/output pass of the forward (backward main kernel for the
     # fwd+bwd workloads); one launch processes every (token, channel) of the call.
+    g0_ = sets[0]
+    from s6scan.selective_scan_interface import _problem, check_inputs
+    z0 = g0_["z"].mT if mixer else None
+    dims = check_inputs(g0_["x"].mT, g0_["delta"].mT, g0_["A"], g0_["B"].mT, g0_["C"].mT,
+                        g0_["D"], z0, None, g0_.get("cu_seqlens"))
+    prob = _problem(g0_["x"].mT, g0_["B"].mT, z0, g0_["D"], None, mixer, dims)
+    single_pass = _lib.LIB.s6_fwd_single_pass(ctypes.byref(prob)) == 1
+    fwd_kernel = ("fwd_lanes (single-pass forward)" if single_pass
+                  else "fwd_scan (output pass of the chunked forward)")
     if cfg.backward:
         dom_name, dom_ms, dom_bytes = "bwd_scan", kb_ms, nbytes - fwd_bytes
     else:
-        dom_name, dom_ms, dom_bytes = "fwd_scan (output pass)", k_ms, fwd_bytes
+        dom_name, dom_ms, dom_bytes = fwd_kernel, k_ms, fwd_bytes
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     # HBM bytes per launch of the dominant kernel and its VALU busy fraction, measured with
     # rocprofv3 (FETCH_SIZE / WRITE_SIZE scaled by a plain-copy calibration; SQ counters) and
     # committed under profiles/.
-    traffic = valu_busy = None
+    traffic = valu_busy = fwd_traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             prof = json.load(f).get(workload)
         if prof:
             traffic = round(prof["traffic_bytes_per_launch"])
             valu_busy = round(prof["kernels"][prof["dominant_kernel"]]["valu_busy"], 3)
+            if prof.get("forward_traffic_bytes") is not None:
+                fwd_traffic = round(prof["forward_traffic_bytes"])
+    prof_src = ("profiles/traffic.json: rocprofv3 --pmc of this workload (FETCH_SIZE, WRITE_SIZE "
+                "scaled by the plain-copy calibration; SQ counters), committed, not measured in "
+                "this run")
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -650,8 +682,10 @@ def measure_scan(torch, workload, steps, warmup):
         "data": "synthetic (seeded normal/uniform inputs of the workload's shape; 3 rotating sets)",
         "config": {"workload": (f"{cfg.name}: SSMMixer S6 core (softplus, D skip, z gate fused; "
                                 "B/C slices of x_proj output)" if mixer else
-                                f"{cfg.name}: selective_scan_fn {'fwd+bwd' if cfg.backward else 'fwd'}"
-                                " on channel-last [B, L, D] views"),
+                                f"{cfg.name}: s6scan selective_scan_forward"
+                                f"{' + selective_scan_backward' if cfg.backward else ''} (the "
+                                "launches selective_scan_fn makes) on channel-last [B, L, D] views"),
+                   "forward_kernel": fwd_kernel,
                    "batch": B, "seqlen": L, "dim": cfg.dim, "dstate": cfg.dstate,
                    "nseq": cfg.nseq, "algorithmic_bytes_per_step": nbytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 5),
@@ -669,8 +703,29 @@ def measure_scan(torch, workload, steps, warmup):
             # The kernels are VALU-bound (exp + 4-5 FMA-class ops per state element, packed
             # FP32 disabled); this is the measured fraction of SIMD cycles issuing VALU work.
             "valu_busy": valu_busy,
+            "traffic_source": prof_src,
+        },
+        # every kernel of the forward call together (for the chunked forward: summaries, carry
+        # and output pass), against the forward's algorithmic bytes
+        "whole_forward": {
+            "gpu_ms": round(fwd_ms, 5),
+            "achieved": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 3),
+            "unit": "GB/s",
+            "frac": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+            "algorithmic_bytes": fwd_bytes,
+            "traffic": fwd_traffic,
+            "traffic_source": prof_src,
         },
     }
+    if cfg.backward:
+        # state checkpoints held from the forward to the backward: fp32 [B, ceil(L/8), D, N]
+        # (the reference's kernel saves [B, D, ceil(L/2048), 2N] fp32 and recomputes within
+        # each 2048-step chunk, selective_scan_interface.py:42-50)
+        nck = -(-L // 8)
+        res["activation_bytes_per_layer"] = {
+            "x_ckpt": B * nck * cfg.dim * cfg.dstate * 4,
+            "reference_x": B * cfg.dim * -(-L // 2048) * 2 * cfg.dstate * 4,
+        }
     if cfg.backward:
         res["fwd_kernel_ms"] = round(k_ms, 5)
     return res
@@ -707,7 +762,13 @@ def main():
         fb = measure_scan(torch, "fwdbwd3", max(10, args.steps // 2), max(3, args.warmup // 2))
         res["fwd_bwd"] = {k: fb[k] for k in ("value", "unit", "ms_per_step", "hbm_frac",
                                               "mtok_ch_per_s", "steps", "config", "roofline",
-                                              "fwd_kernel_ms")}
+                                              "fwd_kernel_ms", "whole_forward",
+                                              "activation_bytes_per_layer")}
+        if not args.no_cpu_baseline:
+            from s6scan.configs import CONFIGS, make_inputs
+            log("cpu baseline (config 3 sample) ...")
+            res["fwd_bwd"]["cpu_baseline"] = cpu_baseline(CONFIGS[3], make_inputs,
+                                                          one_thread=False)
     if not args.no_cpu_baseline:
         from s6scan.configs import CONFIGS, make_inputs
         log("cpu baseline ...")

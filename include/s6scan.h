@@ -155,6 +155,13 @@ int s6_validate_bwd(const S6BwdArgs* a);
  * chunked scan (ssd_combined.py:576-577, ssd_state_passing.py:76-78). */
 int s6_validate_cu_seqlens(const int32_t* cu_host, int64_t nseq, int64_t seqlen);
 
+/* Host-only: 1 if s6_fwd runs this problem on the single-pass kernel (one lane per
+ * (channel, state)), 0 if on the chunked kernels (chunk summaries, carry, output pass), or a
+ * negative code for an invalid problem.  Follows the environment override S6_FWD_PATH=lanes /
+ * chunked as s6_fwd does.  No counterpart in the reference: it names the kernel a caller is
+ * timing or profiling. */
+int s6_fwd_single_pass(const S6Problem* p);
+
 /* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */
 int64_t s6_num_checkpoints(const S6Problem* p);
 

@@ -884,6 +884,12 @@ int s6_validate_problem(const S6Problem* p) {
   return ok();
 }
 
+int s6_fwd_single_pass(const S6Problem* p) {
+  int r = s6_validate_problem(p);
+  if (r != S6_OK) return r;
+  return make_plan(*p, false, nullptr, nullptr, nullptr, nullptr).lanes ? 1 : 0;
+}
+
 int s6_validate_cu_seqlens(const int32_t* cu, int64_t nseq, int64_t seqlen) {
   if (cu == nullptr) return fail(S6_E_INVALID, "cu_seqlens must not be NULL");
   if (nseq < 1 || nseq > (int64_t)INT32_MAX - 1)

@@ -276,3 +276,23 @@ def test_noalloc_forward_rejects_problems_above_its_scratch():
     # argument errors are reported as by s6_fwd
     a.u = None
     assert _lib.LIB.s6_fwd_noalloc(ctypes.byref(a), None) == _lib.E_INVALID
+
+
+def test_forward_kernel_choice(monkeypatch):
+    """s6_fwd_single_pass names the kernel s6_fwd will run: the single-pass kernel for dense
+    batches with enough (channel, state) lanes and no z gate, the chunked kernels otherwise
+    (varlen, small problems, dstate <= 8, the z gate); S6_FWD_PATH forces either."""
+    monkeypatch.delenv("S6_FWD_PATH", raising=False)
+    q = lambda **kw: _lib.LIB.s6_fwd_single_pass(ctypes.byref(prob(**kw)))
+    big = dict(batch=32, dim=256, seqlen=4096, dstate=16)
+    assert q(**big) == 1
+    assert q(**big, has_z=1) == 0
+    assert q(**dict(big, dstate=8)) == 0
+    assert q(batch=1, dim=256, seqlen=4096, dstate=16) == 0          # 64 waves
+    assert q(batch=1, dim=1024, seqlen=4096, dstate=16, nseq=3) == 0  # varlen
+    monkeypatch.setenv("S6_FWD_PATH", "lanes")
+    assert q(batch=1, dim=256, seqlen=4096, dstate=16) == 1
+    assert q(batch=1, dim=1024, seqlen=4096, dstate=16, nseq=3) == 0  # never varlen
+    monkeypatch.setenv("S6_FWD_PATH", "chunked")
+    assert q(**big) == 0
+    assert q(batch=0) == _lib.E_INVALID
