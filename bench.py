@@ -98,52 +98,71 @@ def cpu_config0_one_thread(make_inputs):
             "threads": 1}
 
 
-def cpu_baseline(cfg, make_inputs, mixer=False, one_thread=True, seqlen=None):
-    """Reference CPU path on a bounded sample: one sequence of the workload (4096 steps
-    forward, 2048 steps forward + backward, or ``seqlen``).  The scan workloads time the torch
-    restatement of selective_scan_ref (op for op); the mixer workload the restatement of the
-    reference SSMMixer's own scan loop (backbone.py:1207-1242, state in the input dtype as
-    there)."""
+def cpu_baseline(cfg, make_inputs, mixer=False, one_thread=True, target_s=3.0):
+    """Reference CPU path on a bounded sample of the workload, about 10-20 s of host work.
+    Forward workloads: whole sequences at the workload's seqlen, one call per sequence; a
+    warm-up call on one sequence sets how many (up to the workload's batch) make one timed
+    run last about ``target_s``; the median of 3 timed runs is reported.  Fwd+bwd workloads:
+    one sequence of 1024 steps per call, since the restated path's backward (autograd through
+    the per-step loop, ops/selective_scan_interface.py:138-139, where each step's index of deltaA
+    materialises a full-size gradient) costs O(L^2) per sequence and a full-length sequence
+    would take hours.  The scan workloads time the torch restatement of selective_scan_ref
+    (op for op); the mixer workload the restatement of the reference SSMMixer's own scan loop
+    (backbone.py:1207-1242, state in the input dtype as there)."""
     import dataclasses
 
     import torch
     from oracle.selective_scan_ref import selective_scan_ref, selective_scan_ref_grads
     from oracle.ssm_mixer_ref import ssm_mixer_scan_ref
     torch.set_num_threads(os.cpu_count() or 1)
-    if seqlen is None:
-        seqlen = 2048 if (cfg.backward or not cfg.seqlen) else min(cfg.seqlen, 4096)
-    sample = dataclasses.replace(cfg, batch=1, seqlen=seqlen, nseq=0)
-    inp = make_inputs(sample)
-    args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
-    mix = mixer_extras(torch, inp, torch.Generator("cpu").manual_seed(7)) if mixer else None
+    seqlen = 1024 if cfg.backward else (cfg.seqlen or 8192)
+    nmax = cfg.batch if cfg.seqlen else 64
+    one = dataclasses.replace(cfg, batch=1, seqlen=seqlen, nseq=0)
 
-    def run():
+    def seq_inputs(i):
+        inp = make_inputs(dataclasses.replace(one, seed=cfg.seed + i))
+        mix = (mixer_extras(torch, inp, torch.Generator("cpu").manual_seed(7 + i))
+               if mixer else None)
+        return inp, mix
+
+    def call(inp, mix):
+        args = (inp["x"].mT, inp["delta"].mT, inp["A"], inp["B"].mT, inp["C"].mT)
         if mixer:
             ssm_mixer_scan_ref(inp["x"], mix["dt_raw"], mix["A_log"], mix["B"], mix["C"],
                                inp["D"], mix["z"])
-        elif sample.backward:
+        elif cfg.backward:
             selective_scan_ref_grads(*args, inp["D"], inp["dy"].mT)
         else:
             selective_scan_ref(*args, D=inp["D"], return_last_state=True)
 
-    run()  # warm-up
+    first = seq_inputs(0)
+    t = time.perf_counter()
+    call(*first)  # warm-up, also sizes the sample
+    t1 = time.perf_counter() - t
+    n = max(1, min(nmax, round(target_s / max(t1, 1e-6))))
+    seqs = [first] + [seq_inputs(i) for i in range(1, n)]
     ts = []
     for _ in range(3):
         t = time.perf_counter()
-        run()
+        for inp, mix in seqs:
+            call(inp, mix)
         ts.append(time.perf_counter() - t)
     sec = statistics.median(ts)
+    sample_bytes = n * one.algorithmic_bytes()
+    if mixer:  # + z read, + the gated output, as in the GPU line
+        sample_bytes += 2 * n * seqlen * cfg.dim * first[0]["x"].element_size()
     return {
-        "value": round(sample.algorithmic_bytes() / sec / 1e9, 4),
+        "value": round(sample_bytes / sec / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"restated reference CPU path ("
                    f"{'SSMMixer scan loop' if mixer else 'selective_scan_ref'} op for op"
-                   f"{' + autograd backward' if sample.backward else ''}) on one sequence of "
-                   f"{cfg.name}: batch 1, seqlen {seqlen}, dim {cfg.dim}, dstate {cfg.dstate}; "
-                   f"median of 3 runs = {sec:.3f} s; os.cpu_count() = {os.cpu_count()}"),
-        "mtok_ch_per_s": round(seqlen * cfg.dim / sec / 1e6, 4),
+                   f"{' + autograd backward' if cfg.backward else ''}) on {n} sequence(s) of "
+                   f"{cfg.name}, one call each: seqlen {seqlen}, dim {cfg.dim}, dstate "
+                   f"{cfg.dstate}; median of 3 runs = {sec:.3f} s (warm-up call on one "
+                   f"sequence {t1:.3f} s); os.cpu_count() = {os.cpu_count()}"),
+        "mtok_ch_per_s": round(n * seqlen * cfg.dim / sec / 1e6, 4),
         "cpu_model": cpu_model(),
         **({"config0_one_thread": cpu_config0_one_thread(make_inputs)} if one_thread else {}),
     }
@@ -634,7 +653,7 @@ def measure_scan(torch, workload, steps, warmup):
               else gpu_ms_step)
 
     value = nbytes / (ms_step * 1e-3) / 1e9
-    fwd_bytes = cfg.algorithmic_bytes(seqlen=L, with_backward=False)
+    fwd_bytes = cfg.algorithmic_bytes(seqlen=L, with_backward=False) if cfg.backward else nbytes
     # Dominant kernel: the scan/output pass of the forward (backward main kernel for the
     # fwd+bwd workloads); one launch processes every (token, channel) of the call.
     g0_ = sets[0]
