@@ -23,10 +23,13 @@
  *   initial_states       : [batch, nheads, headdim, dstate] fp32, any strides (optional)
  *   seq_idx              : [batch, seqlen] int32, any strides (optional)
  *   final_states         : [batch, nheads, headdim, dstate] fp32 contiguous (optional out)
- * Rows accessed with 16-byte vector loads and stores (x, z, B, C, out, out_x, dout) need a
- * unit last stride and must start on 16-byte boundaries.
- * Supported: headdim in {32, 64, 128}, dstate in {32, 64, 128, 256}, chunk_size in
- * {64, 128, 256}, io_dtype bf16, fp16 or fp32.  Errors and streams as in s6scan.h.
+ * Supported: headdim 1..128, dstate 1..256, chunk_size 64, 128, 192 or 256, io_dtype bf16,
+ * fp16 or fp32.  The kernels' tiles are headdim 32 / 64 / 128 and dstate 32 / 64 / 128 / 256;
+ * other sizes run on the next tile size up, through zero-padded workspace copies of x, z,
+ * dout (headdim) and B, C (dstate) and padded out, out_x, dx, dz copied back (the workspace
+ * sizes include them).  Rows accessed with 16-byte vector loads and stores need a unit last
+ * stride and must start on 16-byte boundaries: x, z, out, out_x, dout, dx at a tile headdim,
+ * B and C at a tile dstate.  Errors and streams as in s6scan.h.
  */
 #ifndef S6_SSD_H
 #define S6_SSD_H

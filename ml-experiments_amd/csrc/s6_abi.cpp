@@ -451,40 +451,66 @@ int ssu_check(const S6StateUpdateArgs& a) {
 
 struct SsdPlan {
   int64_t K;
-  size_t off_dtq, off_dacs, off_st, off_hs, off_cb, total;
+  // Tile sizes of the kernels: headdim padded to 32 / 64 / 128, dstate to 32 / 64 / 128 / 256.
+  // When they differ from the caller's, x, z, out (, out_x) or B, C are staged through
+  // zero-padded workspace copies; zero columns add nothing to any product.
+  int64_t Pp, Np;
+  bool padP, padN;
+  size_t off_dtq, off_dacs, off_st, off_hs, off_cb;
+  size_t off_Bp, off_Cp, off_xp, off_zp, off_outp, off_outxp, total;
+  size_t off_doutp, off_dxp, off_dzp;
   // backward
   int64_t nE;
   size_t off_dyw, off_dst, off_ddal, off_ddtd, off_dDp, off_qv, off_uv, off_rs, off_csp;
   size_t off_dBp, off_dCp, off_dcb, off_dAp, off_dbp, total_bwd;
 };
 
+int64_t ssd_pad_headdim(int64_t P) { return P <= 32 ? 32 : P <= 64 ? 64 : 128; }
+int64_t ssd_pad_dstate(int64_t N) { return N <= 32 ? 32 : N <= 64 ? 64 : N <= 128 ? 128 : 256; }
+
 SsdPlan ssd_plan(const S6SsdProblem& p) {
   SsdPlan s{};
   s.K = ceil_div(p.seqlen, p.chunk_size);
+  s.Pp = ssd_pad_headdim(p.headdim);
+  s.Np = ssd_pad_dstate(p.dstate);
+  s.padP = s.Pp != p.headdim;
+  s.padN = s.Np != p.dstate;
+  const size_t es = (size_t)esize(p.io_dtype);
   const size_t bhkq = (size_t)(p.batch * p.nheads * s.K * p.chunk_size) * 4;
-  const size_t pn = (size_t)(p.batch * s.K * p.nheads * p.headdim * p.dstate);
+  const size_t pn = (size_t)(p.batch * s.K * p.nheads * s.Pp * s.Np);
+  const size_t lhp = align256((size_t)(p.batch * p.seqlen * p.nheads * s.Pp) * es);
+  const size_t lgn = align256((size_t)(p.batch * p.seqlen * p.ngroups * s.Np) * es);
   size_t off = 0;
   s.off_dtq = off; off += align256(bhkq);
   s.off_dacs = off; off += align256(bhkq);
   s.off_st = off; off += align256(pn * 4);
-  s.off_hs = off; off += align256(pn * (size_t)esize(p.io_dtype));
+  s.off_hs = off; off += align256(pn * es);
   s.off_cb = off; off += align256((size_t)(p.batch * s.K * p.ngroups) * p.chunk_size * p.chunk_size * 4);
+  s.off_Bp = off; off += s.padN ? lgn : 0;
+  s.off_Cp = off; off += s.padN ? lgn : 0;
+  s.off_xp = off; off += s.padP ? lhp : 0;
+  s.off_zp = off; off += (s.padP && p.has_z) ? lhp : 0;
+  s.off_outp = off; off += s.padP ? lhp : 0;
+  s.off_outxp = off; off += (s.padP && p.has_z) ? lhp : 0;
   s.total = off;
+  s.off_doutp = off; off += s.padP ? lhp : 0;
+  s.off_dxp = off; off += s.padP ? lhp : 0;
+  s.off_dzp = off; off += (s.padP && p.has_z) ? lhp : 0;
   const int64_t qt = p.chunk_size / 64;
-  s.nE = p.headdim * p.dstate / 1024;
-  s.off_dyw = off; off += p.has_z ? align256((size_t)(p.batch * p.seqlen * p.nheads * p.headdim) * esize(p.io_dtype)) : 0;
+  s.nE = s.Pp * s.Np / 1024;
+  s.off_dyw = off; off += p.has_z ? lhp : 0;
   s.off_dst = off; off += align256(pn * (size_t)esize(p.io_dtype));
   s.off_ddal = off; off += align256((size_t)(p.batch * p.nheads * s.K * s.nE) * 4);
   s.off_ddtd = off; off += align256(bhkq);
-  s.off_dDp = off; off += align256((size_t)(p.batch * s.K * qt * p.nheads * p.headdim) * 4);
-  const size_t nsl = (size_t)(p.dstate / (p.dstate < 64 ? p.dstate : 64));  // dstate slices of the row kernels
+  s.off_dDp = off; off += align256((size_t)(p.batch * s.K * qt * p.nheads * s.Pp) * 4);
+  const size_t nsl = (size_t)(s.Np / (s.Np < 64 ? s.Np : 64));  // dstate slices of the row kernels
   s.off_qv = off; off += align256(bhkq * nsl);
   s.off_uv = off; off += align256(bhkq * nsl);
   s.off_rs = off; off += align256(bhkq * (size_t)qt);  // one partial per column tile
   s.off_csp = off; off += align256(bhkq * (size_t)qt);
-  const size_t lgn = (size_t)(p.batch * p.seqlen * p.ngroups * p.dstate) * 4;
-  s.off_dBp = off; off += align256(lgn);
-  s.off_dCp = off; off += align256(lgn);
+  const size_t lgn4 = (size_t)(p.batch * p.seqlen * p.ngroups * s.Np) * 4;
+  s.off_dBp = off; off += align256(lgn4);
+  s.off_dCp = off; off += align256(lgn4);
   s.off_dcb = off; off += align256((size_t)(p.batch * s.K * p.ngroups) * p.chunk_size * p.chunk_size * 4);
   s.off_dAp = off; off += align256((size_t)(p.batch * s.K * p.nheads) * 4);
   s.off_dbp = off; off += align256((size_t)(p.batch * s.K * p.nheads) * 4);
@@ -497,12 +523,12 @@ int ssd_check_problem(const S6SsdProblem& p) {
     return fail(S6_E_INVALID, "ssd: batch, seqlen, nheads, ngroups must be >= 1");
   if (p.nheads % p.ngroups != 0)
     return fail(S6_E_INVALID, "ssd: nheads must be divisible by ngroups");
-  if (p.headdim != 32 && p.headdim != 64 && p.headdim != 128)
-    return fail(S6_E_UNSUPPORTED, "ssd: headdim must be 32, 64 or 128, got %lld", (long long)p.headdim);
-  if (p.dstate != 32 && p.dstate != 64 && p.dstate != 128 && p.dstate != 256)
-    return fail(S6_E_UNSUPPORTED, "ssd: dstate must be 32, 64, 128 or 256, got %lld", (long long)p.dstate);
-  if (p.chunk_size != 64 && p.chunk_size != 128 && p.chunk_size != 256)
-    return fail(S6_E_UNSUPPORTED, "ssd: chunk_size must be 64, 128 or 256, got %lld",
+  if (p.headdim < 1 || p.headdim > 128)
+    return fail(S6_E_UNSUPPORTED, "ssd: headdim must be 1..128, got %lld", (long long)p.headdim);
+  if (p.dstate < 1 || p.dstate > 256)
+    return fail(S6_E_UNSUPPORTED, "ssd: dstate must be 1..256, got %lld", (long long)p.dstate);
+  if (p.chunk_size < 64 || p.chunk_size > 256 || p.chunk_size % 64 != 0)
+    return fail(S6_E_UNSUPPORTED, "ssd: chunk_size must be 64, 128, 192 or 256, got %lld",
                 (long long)p.chunk_size);
   if (p.io_dtype != S6_BF16 && p.io_dtype != S6_F16 && p.io_dtype != S6_F32)
     return fail(S6_E_UNSUPPORTED, "ssd: io dtype must be bf16, fp16 or fp32");
@@ -533,17 +559,20 @@ int ssd_check_inputs(const S6SsdProblem& p, const void* x, const int64_t* sx, co
   int r;
   if ((r = ssd_check_problem(p))) return r;
   const int es = esize(p.io_dtype);
+  // tensors staged through padded copies are read element by element: any strides
+  const bool padP = ssd_pad_headdim(p.headdim) != p.headdim;
+  const bool padN = ssd_pad_dstate(p.dstate) != p.dstate;
   if ((r = check_ptr(x, "x")) || (r = check_strides(sx, 4, "x")) ||
-      (r = ssd_check_rows(x, sx, es, "x")) || (r = check_ptr(dt, "dt")) ||
+      (!padP && (r = ssd_check_rows(x, sx, es, "x"))) || (r = check_ptr(dt, "dt")) ||
       (r = check_strides(sdt, 3, "dt")) || (r = check_ptr(A, "A")) || (r = check_ptr(B, "B")) ||
-      (r = check_strides(sB, 4, "B")) || (r = ssd_check_rows(B, sB, es, "B")) ||
+      (r = check_strides(sB, 4, "B")) || (!padN && (r = ssd_check_rows(B, sB, es, "B"))) ||
       (r = check_ptr(C, "C")) || (r = check_strides(sC, 4, "C")) ||
-      (r = ssd_check_rows(C, sC, es, "C")))
+      (!padN && (r = ssd_check_rows(C, sC, es, "C"))))
     return r;
   if (sA < 0) return fail(S6_E_INVALID, "A has a negative stride");
   if (p.has_D && ((r = check_ptr(D, "D")) || (r = check_strides(sD, 2, "D")))) return r;
   if (p.has_z && ((r = check_ptr(z, "z")) || (r = check_strides(sz, 4, "z")) ||
-                   (r = ssd_check_rows(z, sz, es, "z"))))
+                   (!padP && (r = ssd_check_rows(z, sz, es, "z")))))
     return r;
   if (p.has_dt_bias && (r = check_ptr(bias, "dt_bias"))) return r;
   if (p.has_initial_states &&
@@ -555,6 +584,54 @@ int ssd_check_inputs(const S6SsdProblem& p, const void* x, const int64_t* sx, co
 }
 
 s6::SsdK ssd_fill(const S6SsdFwdArgs& a, const SsdPlan& pl);
+
+// Strides of a dense [d0, d1, d2, d3] tensor.
+void dense4(const int64_t d[4], int64_t s[4]) {
+  s[3] = 1;
+  s[2] = d[3];
+  s[1] = d[2] * d[3];
+  s[0] = d[1] * d[2] * d[3];
+}
+
+// Caller tensor (dims `small`, strides `ss`) into the dense padded buffer of dims `big`.
+hipError_t ssd_pad(const void* src, const int64_t ss[4], const int64_t small[4], void* dst,
+                   const int64_t big[4], int es, hipStream_t st) {
+  int64_t ds[4];
+  dense4(big, ds);
+  return s6::launch_copy4d(src, ss, small, dst, ds, big, es, st);
+}
+
+// The leading `small` part of a dense padded buffer (dims `big`) into a caller tensor.
+hipError_t ssd_unpad(const void* src, const int64_t big[4], void* dst, const int64_t ds[4],
+                     const int64_t small[4], int es, hipStream_t st) {
+  int64_t ss[4];
+  dense4(big, ss);
+  return s6::launch_copy4d(src, ss, big, dst, ds, small, es, st);
+}
+
+// Zero-padded copies of the inputs that the plan stages (B, C when dstate is padded; x, z
+// when headdim is), into the buffers ssd_fill pointed the kernels at.
+hipError_t ssd_stage_inputs(const S6SsdFwdArgs& a, const SsdPlan& pl, const s6::SsdK& k,
+                            hipStream_t st) {
+  const S6SsdProblem& p = a.p;
+  const int es = esize(p.io_dtype);
+  hipError_t e = hipSuccess;
+  if (pl.padN) {
+    const int64_t sm[4] = {p.batch, p.seqlen, p.ngroups, p.dstate};
+    const int64_t bg[4] = {p.batch, p.seqlen, p.ngroups, pl.Np};
+    if ((e = ssd_pad(a.B, a.B_stride, sm, const_cast<void*>(k.Bm), bg, es, st)) != hipSuccess ||
+        (e = ssd_pad(a.C, a.C_stride, sm, const_cast<void*>(k.Cm), bg, es, st)) != hipSuccess)
+      return e;
+  }
+  if (pl.padP) {
+    const int64_t sm[4] = {p.batch, p.seqlen, p.nheads, p.headdim};
+    const int64_t bg[4] = {p.batch, p.seqlen, p.nheads, pl.Pp};
+    if ((e = ssd_pad(a.x, a.x_stride, sm, const_cast<void*>(k.x), bg, es, st)) != hipSuccess) return e;
+    if (p.has_z && (e = ssd_pad(a.z, a.z_stride, sm, const_cast<void*>(k.z), bg, es, st)) != hipSuccess)
+      return e;
+  }
+  return e;
+}
 
 }  // namespace
 
@@ -569,12 +646,13 @@ int s6_ssd_validate_fwd(const S6SsdFwdArgs* a) {
                            a->seq_idx_stride);
   if (r) return r;
   const int es = esize(p.io_dtype);
+  const bool padP = ssd_pad_headdim(p.headdim) != p.headdim;
   if ((r = check_ptr(a->out, "out")) || (r = check_strides(a->out_stride, 4, "out")) ||
-      (r = ssd_check_rows(a->out, a->out_stride, es, "out")))
+      (!padP && (r = ssd_check_rows(a->out, a->out_stride, es, "out"))))
     return r;
   if (p.has_z && a->out_x &&
       ((r = check_strides(a->out_x_stride, 4, "out_x")) ||
-       (r = ssd_check_rows(a->out_x, a->out_x_stride, es, "out_x"))))
+       (!padP && (r = ssd_check_rows(a->out_x, a->out_x_stride, es, "out_x")))))
     return r;
   if (a->varlen_states != nullptr) {
     if (p.batch != 1)
@@ -603,7 +681,17 @@ int s6_ssd_fwd(const S6SsdFwdArgs* a, void* stream) {
   const S6SsdProblem& p = a->p;
   const SsdPlan pl = ssd_plan(p);
   s6::SsdK k = ssd_fill(*a, pl);
-  hipError_t e = s6::launch_ssd_fwd(k, (hipStream_t)stream, a->kernel_events);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = ssd_stage_inputs(*a, pl, k, st);
+  if (e == hipSuccess) e = s6::launch_ssd_fwd(k, st, a->kernel_events);
+  if (e == hipSuccess && pl.padP) {
+    const int es = esize(p.io_dtype);
+    const int64_t sm[4] = {p.batch, p.seqlen, p.nheads, p.headdim};
+    const int64_t bg[4] = {p.batch, p.seqlen, p.nheads, pl.Pp};
+    e = ssd_unpad(k.out, bg, a->out, a->out_stride, sm, es, st);
+    if (e == hipSuccess && k.out_x != nullptr)
+      e = ssd_unpad(k.out_x, bg, a->out_x, a->out_x_stride, sm, es, st);
+  }
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_fwd: %s", hipGetErrorString(e));
   return ok();
 }
@@ -617,9 +705,11 @@ int s6_ssd_validate_bwd(const S6SsdBwdArgs* a) {
                            a->seq_idx_stride);
   if (r) return r;
   const int es = esize(p.io_dtype);
+  const bool padP = ssd_pad_headdim(p.headdim) != p.headdim;
   if ((r = check_ptr(a->dout, "dout")) || (r = check_strides(a->dout_stride, 4, "dout")) ||
-      (r = ssd_check_rows(a->dout, a->dout_stride, es, "dout")) ||
+      (!padP && (r = ssd_check_rows(a->dout, a->dout_stride, es, "dout"))) ||
       (r = check_ptr(a->dx, "dx")) || (r = check_strides(a->dx_stride, 4, "dx")) ||
+      (!padP && (r = ssd_check_rows(a->dx, a->dx_stride, es, "dx"))) ||
       (r = check_ptr(a->ddt, "ddt")) || (r = check_strides(a->ddt_stride, 3, "ddt")) ||
       (r = check_ptr(a->dA, "dA")) || (r = check_ptr(a->dB, "dB")) ||
       (r = check_strides(a->dB_stride, 4, "dB")) || (r = check_ptr(a->dC, "dC")) ||
@@ -676,13 +766,38 @@ int s6_ssd_bwd(const S6SsdBwdArgs* a, void* stream) {
   if (p.has_z) {
     k.dyw = ws + pl.off_dyw;
     k.dy = k.dyw;
-    const int64_t P = p.headdim, H = p.nheads, L = p.seqlen;
+    const int64_t P = pl.Pp, H = p.nheads, L = p.seqlen;
     k.sdy[0] = L * H * P; k.sdy[1] = H * P; k.sdy[2] = P; k.sdy[3] = 1;
   } else {
     k.dy = a->dout;
     for (int i = 0; i < 4; ++i) k.sdy[i] = a->dout_stride[i];
   }
   k.dz = p.has_z ? a->dz : nullptr; k.dx = a->dx; k.ddt = a->ddt; k.dBo = a->dB; k.dCo = a->dC;
+  hipStream_t st = (hipStream_t)stream;
+  const int es = esize(p.io_dtype);
+  const int64_t smP[4] = {p.batch, p.seqlen, p.nheads, p.headdim};
+  const int64_t bgP[4] = {p.batch, p.seqlen, p.nheads, pl.Pp};
+  hipError_t e = ssd_stage_inputs(f, pl, k, st);
+  if (e == hipSuccess && pl.padP) {  // dout, the forward's out_x, dx and dz through padded copies
+    int64_t dsP[4];
+    dense4(bgP, dsP);
+    k.dout = ws + pl.off_doutp;
+    for (int i = 0; i < 4; ++i) k.sdout[i] = dsP[i];
+    e = ssd_pad(a->dout, a->dout_stride, smP, ws + pl.off_doutp, bgP, es, st);
+    if (!p.has_z) {
+      k.dy = k.dout;
+      for (int i = 0; i < 4; ++i) k.sdy[i] = dsP[i];
+    }
+    if (e == hipSuccess && p.has_z)  // ssd_fill pointed k.out_x at the padded buffer
+      e = ssd_pad(a->out_x, a->out_x_stride, smP, k.out_x, bgP, es, st);
+    k.dx = ws + pl.off_dxp;
+    if (p.has_z) k.dz = ws + pl.off_dzp;
+    for (int i = 0; i < 4; ++i) {
+      k.sdx[i] = dsP[i];
+      if (p.has_z) k.sdz[i] = dsP[i];
+    }
+  }
+  if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_bwd: %s", hipGetErrorString(e));
   k.dA = a->dA; k.dD = p.has_D ? a->dD : nullptr; k.ddt_bias = p.has_dt_bias ? a->ddt_bias : nullptr;
   k.dinit = a->dinitial_states; k.dfinal = a->dfinal_states;
   k.dhl = k.st;  // the chunk states are consumed by the recomputed state passing first
@@ -691,7 +806,11 @@ int s6_ssd_bwd(const S6SsdBwdArgs* a, void* stream) {
   k.qv = (float*)(ws + pl.off_qv); k.uv = (float*)(ws + pl.off_uv); k.rs = (float*)(ws + pl.off_rs);
   k.csp = (float*)(ws + pl.off_csp); k.dBp = (float*)(ws + pl.off_dBp); k.dCp = (float*)(ws + pl.off_dCp);
   k.dcb = (float*)(ws + pl.off_dcb); k.dAp = (float*)(ws + pl.off_dAp); k.dbp = (float*)(ws + pl.off_dbp);
-  hipError_t e = s6::launch_ssd_bwd(k, (hipStream_t)stream);
+  e = s6::launch_ssd_bwd(k, st);
+  if (e == hipSuccess && pl.padP) {
+    e = ssd_unpad(k.dx, bgP, a->dx, a->dx_stride, smP, es, st);
+    if (e == hipSuccess && p.has_z) e = ssd_unpad(k.dz, bgP, a->dz, a->dz_stride, smP, es, st);
+  }
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_ssd_bwd: %s", hipGetErrorString(e));
   return ok();
 }
@@ -731,6 +850,22 @@ s6::SsdK ssd_fill(const S6SsdFwdArgs& a0, const SsdPlan& pl) {
   char* ws = (char*)a->workspace;
   k.dtq = (float*)(ws + pl.off_dtq); k.dacs = (float*)(ws + pl.off_dacs);
   k.st = (float*)(ws + pl.off_st); k.hs = ws + pl.off_hs; k.cb = (float*)(ws + pl.off_cb);
+  k.P = pl.Pp; k.N = pl.Np; k.Pa = p.headdim; k.Na = p.dstate;
+  if (pl.padN) {
+    const int64_t d[4] = {p.batch, p.seqlen, p.ngroups, pl.Np};
+    k.Bm = ws + pl.off_Bp; k.Cm = ws + pl.off_Cp;
+    dense4(d, k.sB);
+    dense4(d, k.sC);
+  }
+  if (pl.padP) {
+    const int64_t d[4] = {p.batch, p.seqlen, p.nheads, pl.Pp};
+    k.x = ws + pl.off_xp;
+    dense4(d, k.sx);
+    if (p.has_z) { k.z = ws + pl.off_zp; dense4(d, k.sz); }
+    k.out = ws + pl.off_outp;
+    dense4(d, k.sout);
+    if (k.out_x != nullptr) { k.out_x = ws + pl.off_outxp; dense4(d, k.soutx); }
+  }
   return k;
 }
 

@@ -139,6 +139,8 @@ __device__ inline void store_any(void* p, int64_t i, float v, int dt) {
 // Parameter block of the Mamba-2 SSD kernels (strides in elements).
 struct SsdK {
   int64_t Bsz, L, H, P, G, N, Q, K;   // K = number of chunks of Q steps
+  int64_t Pa, Na;  // headdim and dstate of the caller's tensors; P, N: the kernels' tile sizes
+                   // (Pa <= P, Na <= N; x, z, B, C, dout are then zero-padded copies)
   int64_t hpg;                        // heads per B / C group
   int32_t io;                         // dtype of x, z, B, C, dt, out
   int32_t softplus, has_bias, has_D, D_hdim, has_z, has_init, has_seq;
@@ -247,6 +249,11 @@ hipError_t launch_ssd_bwd(const SsdK& k, hipStream_t st);
 hipError_t launch_state_update(const SsuK& k, int state_dtype, bool softplus, bool rows,
                                hipStream_t st);
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st);
+// dst[i] = src[i] for every 4-D index i inside ddim, 0 where i lies outside sdim (strides in
+// elements, esize 2 or 4): zero-pads a tensor into a larger buffer, or copies the leading part
+// of a padded buffer out.
+hipError_t launch_copy4d(const void* src, const int64_t ss[4], const int64_t sdim[4], void* dst,
+                         const int64_t ds[4], const int64_t ddim[4], int esize, hipStream_t st);
 hipError_t launch_relayout(const void* src, const int64_t s[4], int esize, void* dst,
                            int64_t Bsz, int64_t G, int64_t N, int64_t NP, int64_t L,
                            hipStream_t st);

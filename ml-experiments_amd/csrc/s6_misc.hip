@@ -143,6 +143,29 @@ __global__ void relayout_bc(const T* __restrict__ src, int64_t s0, int64_t s1, i
   }
 }
 
+struct Dims4 {
+  int64_t v[4];
+};
+
+// dst[i] = src[i] inside sd, 0 outside, for every 4-D index i inside dd; innermost axis fastest.
+template <typename T>
+__global__ void copy4d(const T* __restrict__ src, Dims4 ss, Dims4 sd, T* __restrict__ dst, Dims4 ds,
+                       Dims4 dd) {
+  const int64_t total = dd.v[0] * dd.v[1] * dd.v[2] * dd.v[3];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = i;
+    const int64_t i3 = r % dd.v[3]; r /= dd.v[3];
+    const int64_t i2 = r % dd.v[2]; r /= dd.v[2];
+    const int64_t i1 = r % dd.v[1];
+    const int64_t i0 = r / dd.v[1];
+    T v{};
+    if (i0 < sd.v[0] && i1 < sd.v[1] && i2 < sd.v[2] && i3 < sd.v[3])
+      v = src[i0 * ss.v[0] + i1 * ss.v[1] + i2 * ss.v[2] + i3 * ss.v[3]];
+    dst[i0 * ds.v[0] + i1 * ds.v[1] + i2 * ds.v[2] + i3 * ds.v[3]] = v;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 
 static unsigned grid_for(int64_t total, int64_t threads) {
@@ -180,6 +203,24 @@ hipError_t launch_bwd_reduce(const BwdK& k, hipStream_t st) {
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_f32, dim3(grid_for(n, 256)), dim3(256), 0, st, p, n, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy4d(const void* src, const int64_t ss[4], const int64_t sdim[4], void* dst,
+                         const int64_t ds[4], const int64_t ddim[4], int esize, hipStream_t st) {
+  const int64_t total = ddim[0] * ddim[1] * ddim[2] * ddim[3];
+  if (total <= 0) return hipSuccess;
+  Dims4 a, b, c, d;
+  for (int i = 0; i < 4; ++i) {
+    a.v[i] = ss[i]; b.v[i] = sdim[i]; c.v[i] = ds[i]; d.v[i] = ddim[i];
+  }
+  const dim3 grid(grid_for(total, 256));
+  if (esize == 4)
+    hipLaunchKernelGGL(copy4d<uint32_t>, grid, dim3(256), 0, st, (const uint32_t*)src, a, b,
+                       (uint32_t*)dst, c, d);
+  else
+    hipLaunchKernelGGL(copy4d<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, a, b,
+                       (uint16_t*)dst, c, d);
   return hipGetLastError();
 }
 

@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(kThreads)
   if constexpr (MODE == 2) {
     const Raw* hin = (const Raw*)k.hs + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
     const float sc = carry ? exp_split(s_last) : 0.f;
-    Raw* out = (Raw*)k.vst + ((wid / k.H) * k.H + hh) * (int64_t)(P * N);
+    Raw* out = (Raw*)k.vst + ((wid / k.H) * k.H + hh) * (k.Pa * k.Na);  // [nseq, H, Pa, Na]
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int ti = w + 4 * i;
@@ -246,9 +246,9 @@ __global__ void __launch_bounds__(kThreads)
         const int pt = ti / NTN, nt = ti % NTN;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int o = (pt * 16 + 4 * (lane >> 4) + j) * N + nt * 16 + (lane & 15);
-          const float v = carry ? fmaf(M::from_raw(hin[o]), sc, acc[i][j]) : acc[i][j];
-          out[o] = M::to_raw(v);
+          const int pr = pt * 16 + 4 * (lane >> 4) + j, nc = nt * 16 + (lane & 15);
+          const float v = carry ? fmaf(M::from_raw(hin[pr * N + nc]), sc, acc[i][j]) : acc[i][j];
+          if (pr < k.Pa && nc < k.Na) out[pr * k.Na + nc] = M::to_raw(v);
         }
       }
     }
@@ -284,7 +284,8 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass(SsdK k) {
   for (int i = 0; i < kSpEpt; ++i) {
     e[i] = (int64_t)blockIdx.x * (kThreads * kSpEpt) + threadIdx.x + i * kThreads;
     const int64_t p = e[i] / k.N, n = e[i] % k.N;
-    H[i] = k.has_init ? k.init[b * k.sinit[0] + hh * k.sinit[1] + p * k.sinit[2] + n * k.sinit[3]] : 0.f;
+    H[i] = (k.has_init && p < k.Pa && n < k.Na)
+               ? k.init[b * k.sinit[0] + hh * k.sinit[1] + p * k.sinit[2] + n * k.sinit[3]] : 0.f;
   }
   Raw* hs = (Raw*)k.hs;
   const float* sl = k.dacs + (b * k.H + hh) * k.K * k.Q + k.Q - 1;  // S_last of chunk c: sl[c * Q]
@@ -321,9 +322,12 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass(SsdK k) {
     step(c, sa, la);
     if (c + 1 < k.K) step(c + 1, sb, lb);
   }
-  if (k.final_states) {
+  if (k.final_states) {  // [Bsz, H, Pa, Na]
 #pragma unroll
-    for (int i = 0; i < kSpEpt; ++i) k.final_states[(b * k.H + hh) * PN + e[i]] = H[i];
+    for (int i = 0; i < kSpEpt; ++i) {
+      const int64_t p = e[i] / k.N, n = e[i] % k.N;
+      if (p < k.Pa && n < k.Na) k.final_states[((b * k.H + hh) * k.Pa + p) * k.Na + n] = H[i];
+    }
   }
 }
 
@@ -580,7 +584,8 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
       load16<T>(xbase + (l * k.sx[1] + col) * ES, xr);
 #pragma unroll
       for (int q = 0; q < VE; ++q) {
-        const float Dv = k.D_hdim ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : k.Dp[hh * k.sD[0]];
+        const float Dv = !k.D_hdim ? k.Dp[hh * k.sD[0]]
+                         : col + q < k.Pa ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : 0.f;
         y[q] = fmaf(Dv, M::from_raw(xr[q]), y[q]);
       }
     }

@@ -77,7 +77,8 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_bwd(SsdK k) {
   for (int i = 0; i < kSpbPer; ++i) {
     e[i] = eb * (kThreads * kSpbPer) + tid + i * kThreads;  // PN is a multiple of 1024
     const int64_t p = e[i] / k.N, n = e[i] % k.N;
-    dH[i] = k.dfinal ? k.dfinal[b * k.sdfinal[0] + hh * k.sdfinal[1] + p * k.sdfinal[2] + n * k.sdfinal[3]] : 0.f;
+    dH[i] = (k.dfinal && p < k.Pa && n < k.Na)
+                ? k.dfinal[b * k.sdfinal[0] + hh * k.sdfinal[1] + p * k.sdfinal[2] + n * k.sdfinal[3]] : 0.f;
   }
   const Raw* hs = (const Raw*)k.hs;
   Raw* dst = (Raw*)k.dst;
@@ -123,9 +124,12 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_bwd(SsdK k) {
     }
     __syncthreads();
   }
-  if (k.dinit) {
+  if (k.dinit) {  // [Bsz, H, Pa, Na]
 #pragma unroll
-    for (int i = 0; i < kSpbPer; ++i) k.dinit[(b * k.H + hh) * PN + e[i]] = dH[i];
+    for (int i = 0; i < kSpbPer; ++i) {
+      const int64_t p = e[i] / k.N, n = e[i] % k.N;
+      if (p < k.Pa && n < k.Na) k.dinit[((b * k.H + hh) * k.Pa + p) * k.Na + n] = dH[i];
+    }
   }
 }
 
@@ -326,7 +330,8 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   float Dv[VE];
 #pragma unroll
   for (int q = 0; q < VE; ++q)
-    Dv[q] = !k.has_D ? 0.f : k.D_hdim ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : k.Dp[hh * k.sD[0]];
+    Dv[q] = !k.has_D ? 0.f : !k.D_hdim ? k.Dp[hh * k.sD[0]]
+            : col + q < k.Pa ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : 0.f;
   for (int e = tid; e < 64 * RPT; e += kThreads) {  // uniform trip count over the block
     const int r = e / RPT;
     const int s = lt * 64 + r;
@@ -780,6 +785,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_bmm(SsdK k) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int n = nt * 16 + (lane & 15);
+      if (n >= k.Na) continue;  // padded dstate column
       const float v = acc[nt][j] + part[((b * k.L + t0 + l) * k.G + g) * N + n];
       Elem<T>::store(outp, b * sop[0] + (t0 + l) * sop[1] + g * sop[2] + n, v);
     }
@@ -897,7 +903,11 @@ __global__ void __launch_bounds__(kWave) ssd_bwd_reduce(SsdK k) {
   if (lane != 0) return;
   if (o < k.H) k.dA[o] = s;
   else if (o < 2 * k.H) { if (k.ddt_bias) k.ddt_bias[o - k.H] = s; }
-  else k.dD[o - 2 * k.H] = s;
+  else if (!k.D_hdim) k.dD[o - 2 * k.H] = s;
+  else {  // [H, Pa]
+    const int64_t i = o - 2 * k.H, p = i % k.P;
+    if (p < k.Pa) k.dD[(i / k.P) * k.Pa + p] = s;
+  }
 }
 
 // ---- dispatch ------------------------------------------------------------------------

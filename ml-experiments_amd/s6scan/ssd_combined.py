@@ -21,8 +21,9 @@ ssd_combined.py:563-582, forward :281-332):
 The forward runs five HIP kernels (chunk cumsum, chunk states and C B^T on MFMA, state
 passing, the chunk scan on MFMA; ml-experiments_amd/csrc/s6_ssd.hip); the backward recomputes
 the chunk quantities and runs ten more (s6_ssd_bwd.hip), deterministic.  Supported
-shapes: headdim 32 / 64 / 128, dstate 32 / 64 / 128 / 256, chunk_size 64 / 128 / 256.
-There is no CPU path.
+shapes: headdim 1..128, dstate 1..256 (the kernels' tiles are 32 / 64 / 128 and 32 / 64 /
+128 / 256; other sizes run on zero-padded copies inside the library), chunk_size 64, 128, 192
+or 256.  There is no CPU path.
 """
 import ctypes
 import math
@@ -42,10 +43,16 @@ def _st(t, n):
     return tuple(t.stride()) if t is not None else (0,) * n
 
 
-def _rows16(t):
+_TILES = {"headdim": (32, 64, 128), "dstate": (32, 64, 128, 256)}
+
+
+def _rows16(t, axis="headdim"):
     """t with unit last stride and 16-byte aligned rows (a contiguous copy otherwise), as
     the reference makes B / C / x contiguous when their last stride is not 1
-    (ssd_combined.py:297-304)."""
+    (ssd_combined.py:297-304).  Off the kernels' tile sizes the library copies the tensor
+    into a zero-padded buffer element by element, at any strides, so t is passed as it is."""
+    if t.shape[-1] not in _TILES[axis]:
+        return t
     es = t.element_size()
     ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
           and all((s * es) % 16 == 0 for s in t.stride()[:-1]))
@@ -87,7 +94,7 @@ def _prepare(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx):
     if x.dtype not in _DTYPES:
         raise NotImplementedError(f"mamba_chunk_scan_combined: dtype {x.dtype} (bf16, fp16 or fp32 only)")
     dtype = x.dtype
-    x, B, C = _rows16(x), _rows16(B.to(dtype)), _rows16(C.to(dtype))
+    x, B, C = _rows16(x), _rows16(B.to(dtype), "dstate"), _rows16(C.to(dtype), "dstate")
     if z is not None:
         z = _rows16(z.to(dtype))
     f32 = lambda t: None if t is None else t.float()

@@ -296,3 +296,39 @@ def test_forward_kernel_choice(monkeypatch):
     monkeypatch.setenv("S6_FWD_PATH", "chunked")
     assert q(**big) == 0
     assert q(batch=0) == _lib.E_INVALID
+
+
+def _ssd_problem(P=64, N=32, Q=64, z=0, L=300, H=4, G=2, batch=2):
+    return _lib.S6SsdProblem(batch, L, H, P, G, N, Q, _lib.BF16, 1, 0, z, 1, 1, 0, 0, 0.0,
+                             float("inf"))
+
+
+@pytest.mark.parametrize("shape", [(160, 32, 64), (0, 32, 64), (64, 300, 64), (64, 0, 64),
+                                   (64, 32, 32), (64, 32, 100), (64, 32, 320)])
+def test_ssd_shape_limits_rejected(shape):
+    """headdim above 128, dstate above 256 and chunk sizes that are not 64, 128, 192 or 256
+    have no kernel: the workspace query says so (0) before any launch."""
+    P, N, Q = shape
+    assert _lib.LIB.s6_ssd_fwd_workspace_bytes(ctypes.byref(_ssd_problem(P, N, Q))) == 0
+    assert _lib.LIB.s6_ssd_bwd_workspace_bytes(ctypes.byref(_ssd_problem(P, N, Q))) == 0
+
+
+@pytest.mark.parametrize("z", [0, 1])
+def test_ssd_padded_shapes_accepted_with_staging_buffers(z):
+    """Shapes off the kernels' tiles (zoology Mamba-2's d_state 8 / 16 / 24, headdim 48,
+    chunk 192) are accepted; their workspace is the next tile shape's plus the zero-padded
+    copies: B and C at dstate 24 (-> 32), and x, out (z, out_x) at headdim 48 (-> 64), plus
+    dout, dx (dz) in the backward."""
+    ws = lambda f, *a, **k: getattr(_lib.LIB, f)(ctypes.byref(_ssd_problem(*a, z=z, **k)))
+    al = lambda n: (n + 255) // 256 * 256
+    batch, L, H, G = 2, 300, 4, 2
+    for f in ("s6_ssd_fwd_workspace_bytes", "s6_ssd_bwd_workspace_bytes"):
+        assert ws(f, 64, 32, 192) > 0
+        for N in (8, 16, 24):
+            assert ws(f, 64, N, 256) == ws(f, 64, 32, 256) + 2 * al(batch * L * G * 32 * 2)
+    nP = 2 + 2 * z  # x, out (, z, out_x)
+    assert (ws("s6_ssd_fwd_workspace_bytes", 48, 32, 64)
+            == ws("s6_ssd_fwd_workspace_bytes", 64, 32, 64) + nP * al(batch * L * H * 64 * 2))
+    nPb = nP + 2 + z  # + dout, dx (, dz)
+    assert (ws("s6_ssd_bwd_workspace_bytes", 48, 32, 64)
+            == ws("s6_ssd_bwd_workspace_bytes", 64, 32, 64) + nPb * al(batch * L * H * 64 * 2))

@@ -108,10 +108,109 @@ def test_ssd_mamba2_defaults_bf16():
     check(out, ref, torch.bfloat16, "out")
 
 
-def test_ssd_rejects_unsupported_shapes():
-    t, kw = make(1, 64, 1, 48, 1, 32, torch.float32, seed=1)
-    with pytest.raises(RuntimeError, match="headdim"):
-        ssd_forward(**{k: v.to(DEV) for k, v in t.items()}, chunk_size=64, **kw)
+@pytest.mark.parametrize("shape,what", [((160, 32, 64), "headdim"), ((64, 300, 64), "dstate"),
+                                        ((64, 32, 32), "chunk_size"), ((64, 32, 100), "chunk_size")])
+def test_ssd_rejects_unsupported_shapes(shape, what):
+    P, N, Q = shape
+    t, kw = make(1, 64, 1, P, 1, N, torch.float32, seed=1)
+    with pytest.raises(RuntimeError, match=what):
+        ssd_forward(**{k: v.to(DEV) for k, v in t.items()}, chunk_size=Q, **kw)
+
+
+# Shapes off the kernels' tiles (headdim 32 / 64 / 128, dstate 32 / 64 / 128 / 256), which run
+# on zero-padded copies: zoology's Mamba-2 sweep (models_repo.py:131-137: d_state 8 / 16 / 24,
+# mamba2.py:35-53: headdim 64, chunk_size 256; d_model 64 / 128 / 256 give 2 / 4 / 8 heads),
+# chunk 64, other headdims, and chunk 192.
+PAD_CASES = [  # batch, L, H, P, G, N, chunk, opts
+    (2, 256, 4, 64, 1, 16, 256, ("D", "bias", "final")),
+    (2, 300, 2, 64, 1, 24, 64, ("z", "D", "bias", "init", "final")),
+    (1, 700, 8, 64, 1, 8, 256, ("D_hdim", "seq", "bias")),
+    (2, 333, 4, 64, 2, 24, 256, ("z", "bias", "limit")),
+    (2, 200, 4, 48, 2, 16, 64, ("z", "D_hdim", "init", "final")),
+    (1, 400, 3, 80, 1, 40, 192, ("D", "bias", "seq", "final")),
+    (2, 130, 2, 24, 1, 100, 128, ("z", "init", "final", "limit")),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", PAD_CASES, ids=lambda c: "-".join(map(str, c[:7])))
+def test_ssd_padded_shapes_forward_and_backward(case, dtype):
+    batch, L, H, P, G, N, Q, opts = case
+    t, kw = make(batch, L, H, P, G, N, dtype, seed=L + 7 * N + P, opts=opts)
+    final = "final" in opts
+    g = torch.Generator().manual_seed(L + 2)
+    dy = torch.randn(batch, L, H, P, generator=g)
+    dfin = torch.randn(batch, H, P, N, generator=g)
+    names = [k for k, v in t.items() if v.is_floating_point()]
+    gpu = {k: (v.to(DEV).requires_grad_(True) if k in names else v.to(DEV)) for k, v in t.items()}
+    res = mamba_chunk_scan_combined(**gpu, chunk_size=Q, return_final_states=final, **kw)
+    out, fin = res if final else (res, None)
+    cpu = {k: (v.double().requires_grad_(True) if k in names else v) for k, v in t.items()}
+    ref, _, ref_fin = ssd_chunked_ref(**cpu, chunk_size=Q, compute_dtype=torch.float64, **kw)
+    assert out.shape == (batch, L, H, P) and out.dtype == dtype
+    check(out, ref.detach(), dtype, "out")
+    if final:
+        assert fin.shape == (batch, H, P, N)
+        check(fin, ref_fin.detach(), torch.float32 if dtype == torch.float32 else dtype, "final_states")
+    loss = (out.float() * dy.to(DEV)).sum() + ((fin * dfin.to(DEV)).sum() if final else 0.0)
+    loss.backward()
+    rloss = (ref * dy.double()).sum() + ((ref_fin * dfin.double()).sum() if final else 0.0)
+    rloss.backward()
+    if dtype == torch.float32:
+        # dA and ddt_bias sum over every step of the batch with heavy cancellation, so their
+        # fp32 error depends on the order of the sum: the bound adds twice the worst error of
+        # the reference's own fp32 evaluation (the same restatement in float32 autograd)
+        c32 = {k: (v.detach().clone().requires_grad_(True) if k in names else v) for k, v in t.items()}
+        r32, _, r32_fin = ssd_chunked_ref(**c32, chunk_size=Q, compute_dtype=torch.float32, **kw)
+        ((r32 * dy).sum() + ((r32_fin * dfin).sum() if final else 0.0)).backward()
+    for k in names:
+        assert gpu[k].grad.shape == t[k].shape and gpu[k].grad.dtype == t[k].dtype, k
+        if dtype == torch.float32:
+            e32 = (c32[k].grad.double() - cpu[k].grad).abs().max().item()
+            ref_g = cpu[k].grad
+            assert_close(gpu[k].grad, ref_g, 1e-4, 1e-4 * rms(ref_g) + 2 * e32, "d" + k)
+        else:
+            check_grad(gpu[k].grad, cpu[k].grad, dtype, "d" + k)
+
+
+def test_ssd_padded_shapes_strided_views():
+    """Padded shapes read any strides: x, B, C as views of one [batch, L, H P + 2 G N] buffer
+    whose rows are not 16-byte multiples (headdim 40, dstate 12, bf16), and out_x / z through
+    the z gate; the result equals the one from contiguous copies bit for bit."""
+    batch, L, H, P, G, N = 2, 260, 2, 40, 1, 12
+    g = torch.Generator().manual_seed(9)
+    buf = torch.randn(batch, L, H * P + 2 * G * N + 3, generator=g).to(torch.bfloat16).to(DEV)
+    x = buf[..., 3:3 + H * P].unflatten(-1, (H, P))
+    B = buf[..., 3 + H * P:3 + H * P + G * N].unflatten(-1, (G, N))
+    C = buf[..., 3 + H * P + G * N:].unflatten(-1, (G, N))
+    dt = (0.5 * torch.randn(batch, L, H, generator=g) - 1.0).to(torch.bfloat16).to(DEV)
+    A = (-torch.exp(torch.rand(H, generator=g) * 2.77)).to(DEV)
+    z = torch.randn(batch, L, H, P, generator=g).to(torch.bfloat16).to(DEV)
+    kw = dict(D=torch.randn(H, generator=g).to(DEV), dt_softplus=True)
+    a = mamba_chunk_scan_combined(x, dt, A, B, C, 64, z=z, **kw)
+    b = mamba_chunk_scan_combined(x.contiguous(), dt, A, B.contiguous(), C.contiguous(), 64, z=z, **kw)
+    assert torch.equal(a, b)
+    ref, _, _ = ssd_chunked_ref(x.cpu(), dt.cpu(), A.cpu(), B.cpu(), C.cpu(), 64, z=z.cpu(),
+                                D=kw["D"].cpu(), dt_softplus=True, compute_dtype=torch.float64)
+    check(a, ref, torch.bfloat16, "out")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ssd_varlen_states_padded_shapes(dtype):
+    from oracle.ssd_ref import ssd_varlen_states_ref
+    cu = [0, 50, 64, 200, 201, 513, 700]
+    t, kw = make(1, 700, 2, 48, 1, 24, dtype, seed=78, opts=("bias", "D", "init"))
+    gpu = {k: v.to(DEV) for k, v in t.items()}
+    out, vst = mamba_chunk_scan_combined(
+        **gpu, chunk_size=64, cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=DEV),
+        return_varlen_states=True, **kw)
+    assert vst.shape == (len(cu) - 1, 2, 48, 24) and vst.dtype == dtype
+    ref = ssd_varlen_states_ref(t["x"].double(), t["dt"].double(), t["A"].double(),
+                                t["B"].double(), 64, torch.tensor(cu),
+                                dt_bias=t["dt_bias"].double(),
+                                initial_states=t["initial_states"].double(),
+                                compute_dtype=torch.float64, **kw)
+    check(vst, ref, dtype, "varlen_states")
 
 
 GRAD_CASES = [  # batch, L, H, P, G, N, chunk, opts
