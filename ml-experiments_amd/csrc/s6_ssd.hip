@@ -404,13 +404,17 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   constexpr int XPT = P + 16;                              // row-major x pitch (TR)
   constexpr int XS_BYTES = TR ? 2 * KST * XPT * ES : 2 * P * LP * ES;
   constexpr int YS_BYTES = 64 * YP * 4, HS_BYTES = P * HP * ES;
-  constexpr int SM_A = XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES;
+  // 16-bit types with 64-step stages (headdim <= 64): the intra loop's last stage is the
+  // block's own 64 rows of x, so the D skip reads them from that LDS buffer instead of global
+  // memory, and y gets its own staging area after the x buffers.
+  constexpr bool XKEEP = TR && KST == 64 && P <= 64;
+  constexpr int SM_A = XKEEP ? XS_BYTES + YS_BYTES : (XS_BYTES > YS_BYTES ? XS_BYTES : YS_BYTES);
   constexpr int SM_BYTES = SM_A > HS_BYTES ? SM_A : HS_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[SM_BYTES];
   __shared__ float sls[2][KST], dls[2][KST];
   Raw (*xs)[P][LP] = reinterpret_cast<Raw (*)[P][LP]>(smem);
   Raw (*xr)[KST][XPT] = reinterpret_cast<Raw (*)[KST][XPT]>(smem);
-  float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem);
+  float (*ys)[YP] = reinterpret_cast<float (*)[YP]>(smem + (XKEEP ? XS_BYTES : 0));
   Raw (*hsm)[HP] = reinterpret_cast<Raw (*)[HP]>(smem);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // work id -> (head fastest, row tile, chunk, batch): one (batch, chunk)'s blocks, which
@@ -451,9 +455,19 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
     }
 #pragma unroll
     for (int ks = 0; ks < SUB; ++ks) {
-      const bool reach = s0 + ks * kKs <= rowbase + 15;  // wave-uniform
+      if constexpr (TR) {
+        // this lane's 8 consecutive CB values of the slice, as two 16-byte loads: 16-byte
+        // aligned (the chunk size is a multiple of 64) and inside the chunk's Q x Q tile
+        // (s0 + KST <= Q); slices past the wave's rows are loaded but not used
+        const float4* src = reinterpret_cast<const float4*>(cbrow + s0 + ks * kKs + 8 * (lane >> 4));
+        const float4 lo = src[0], hi = src[1];
+        cbv[ks][0] = lo.x; cbv[ks][1] = lo.y; cbv[ks][2] = lo.z; cbv[ks][3] = lo.w;
+        cbv[ks][4] = hi.x; cbv[ks][5] = hi.y; cbv[ks][6] = hi.z; cbv[ks][7] = hi.w;
+      } else {
+        const bool reach = s0 + ks * kKs <= rowbase + 15;  // wave-uniform
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cbv[ks][j] = reach ? cbrow[s0 + ks * kKs + M::kidx(lane, j)] : 0.f;
+        for (int j = 0; j < 8; ++j) cbv[ks][j] = reach ? cbrow[s0 + ks * kKs + M::kidx(lane, j)] : 0.f;
+      }
     }
   };
   fetch(0);
@@ -580,13 +594,16 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
 #pragma unroll
     for (int q = 0; q < VE; ++q) y[q] = ys[r][col + q];
     if (k.has_D) {
-      Raw xr[VE];
-      load16<T>(xbase + (l * k.sx[1] + col) * ES, xr);
+      Raw xl[VE];
+      if constexpr (XKEEP)  // the last stage (rows lt * 64 ..) is still in its LDS buffer
+        *reinterpret_cast<u4*>(xl) = *reinterpret_cast<const u4*>(&xr[(nst - 1) & 1][r][col]);
+      else
+        load16<T>(xbase + (l * k.sx[1] + col) * ES, xl);
 #pragma unroll
       for (int q = 0; q < VE; ++q) {
         const float Dv = !k.D_hdim ? k.Dp[hh * k.sD[0]]
                          : col + q < k.Pa ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : 0.f;
-        y[q] = fmaf(Dv, M::from_raw(xr[q]), y[q]);
+        y[q] = fmaf(Dv, M::from_raw(xl[q]), y[q]);
       }
     }
     Raw o[VE];
