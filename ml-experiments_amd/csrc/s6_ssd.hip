@@ -149,7 +149,11 @@ __global__ void __launch_bounds__(kThreads)
   const char* bbase = (const char*)(MODE != 1 ? k.Bm : k.Cm) + (b * sbr[0] + t0 * sbr[1] + g * sbr[2]) * ES;
 
   Raw xv[XL][VE], bv[BL][VE];
-  float wv[BL];
+  // The weight inputs of each B row (dt', the cumsum, the seq_idx value) stay raw until the
+  // slice is written to LDS: a weight formed right after its loads would wait for them there,
+  // one full memory latency per slice.
+  float dqv[BL], sqv[BL];
+  int32_t sqi[BL];
   // Loads of the slice starting at l0 into registers; rows past the sequence end read as 0.
   auto fetch = [&](int l0) {
 #pragma unroll
@@ -166,11 +170,15 @@ __global__ void __launch_bounds__(kThreads)
       const int e = tid + i * kThreads;
       const int r = e / (N / VE), col = (e % (N / VE)) * VE;
       const int l = l0 + r;
-      wv[i] = 0.f;
+      dqv[i] = 0.f;  // weight 0 past the sequence end
+      sqv[i] = 0.f;
+      sqi[i] = seq_ref;
       if (e < BC && l < lim) {
         load16<T>(bbase + (l * sbr[1] + col) * ES, bv[i]);
-        wv[i] = MODE != 1 ? dq[l] * exp_split(s_last - sq[l]) : exp_split(sq[l]);
-        if (MODE == 2 ? l < rstart : (k.has_seq && seq_at(k, b, t0 + l) != seq_ref)) wv[i] = 0.f;
+        dqv[i] = MODE != 1 ? dq[l] : 1.f;
+        sqv[i] = sq[l];
+        if (MODE != 2 && k.has_seq) sqi[i] = seq_at(k, b, t0 + l);
+        if (MODE == 2 && l < rstart) dqv[i] = 0.f;
       } else {
 #pragma unroll
         for (int q = 0; q < VE; ++q) bv[i][q] = M::to_raw(0.f);
@@ -205,9 +213,11 @@ __global__ void __launch_bounds__(kThreads)
       const int e = tid + i * kThreads;
       if (e < BC) {
         const int r = e / (N / VE), col = (e % (N / VE)) * VE;
+        float wgt = dqv[i] * exp_split(MODE != 1 ? s_last - sqv[i] : sqv[i]);
+        if (MODE != 2 && k.has_seq && sqi[i] != seq_ref) wgt = 0.f;
         Raw o[VE];
 #pragma unroll
-        for (int q = 0; q < VE; ++q) o[q] = M::to_raw(M::from_raw(bv[i][q]) * wv[i]);
+        for (int q = 0; q < VE; ++q) o[q] = M::to_raw(M::from_raw(bv[i][q]) * wgt);
         if constexpr (TR) {
           *reinterpret_cast<u4*>(&br[buf][r][col]) = *reinterpret_cast<const u4*>(o);
         } else {
