@@ -481,6 +481,16 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
     }
   };
   fetch(0);
+  // Values used only after the state term: loaded here, with the first stage, so that no
+  // later step waits a full memory latency for them.
+  const float s_row = row < lim ? sq[row] : 0.f;  // S of this lane's A-operand row
+  float s_acc[4];                                  // S of this lane's accumulator rows
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int l = rowbase + 4 * (lane >> 4) + j;
+    s_acc[j] = l < lim ? sq[l] : 0.f;
+  }
+  const float D_head = (k.has_D && !k.D_hdim) ? k.Dp[hh * k.sD[0]] : 0.f;
 
   f4 acc[PT];
 #pragma unroll
@@ -528,7 +538,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
       const int l = rowbase + 4 * (lane >> 4) + j;
       float f = 0.f;
       if (l < lim) {
-        f = exp_split(sq[l]);
+        f = exp_split(s_acc[j]);
         if (k.has_seq && seq_at(k, b, t0 + l) != seq_prev) f = 0.f;
       }
 #pragma unroll
@@ -537,7 +547,6 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   }
 
   // (b) within the chunk: sum_{s <= l} CB[l, s] e^{S_l - S_s} dt'_s x_s
-  const float s_row = row < lim ? sq[row] : 0.f;
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
     const int s0 = st * KST;
@@ -611,7 +620,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
         load16<T>(xbase + (l * k.sx[1] + col) * ES, xl);
 #pragma unroll
       for (int q = 0; q < VE; ++q) {
-        const float Dv = !k.D_hdim ? k.Dp[hh * k.sD[0]]
+        const float Dv = !k.D_hdim ? D_head
                          : col + q < k.Pa ? k.Dp[hh * k.sD[0] + (col + q) * k.sD[1]] : 0.f;
         y[q] = fmaf(Dv, M::from_raw(xl[q]), y[q]);
       }

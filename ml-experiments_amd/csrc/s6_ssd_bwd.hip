@@ -214,6 +214,16 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
     }
   };
   fetch(lt * 64);
+  // Values used only after the T2 product: loaded here, with the first stage, so that no
+  // later step waits a full memory latency for them.
+  const float s_last = sq[k.Q - 1];
+  const float s_row = row < lim ? sq[row] : 0.f;  // S of this lane's A-operand row
+  float s_acc[4];                                  // S of this lane's accumulator rows
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s = rowbase + 4 * (lane >> 4) + j;
+    s_acc[j] = s < lim ? sq[s] : 0.f;
+  }
 
   f4 acc[PT];
 #pragma unroll
@@ -252,14 +262,13 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
           M::mma(acc[pt], af[i], M::load_row(&dsm[pt * 16 + (lane & 15)][i * kKs], lane));
     }
     __syncthreads();  // dst consumed before the T1 loop writes dy over it
-    const float s_last = sq[k.Q - 1];
     const int32_t seq_last = k.has_seq ? seq_last_of(k, b, c) : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int s = rowbase + 4 * (lane >> 4) + j;
       float f = 0.f;
       if (s < lim) {
-        f = exp_split(s_last - sq[s]);
+        f = exp_split(s_last - s_acc[j]);
         if (k.has_seq && seq_at(k, b, t0 + s) != seq_last) f = 0.f;
       }
 #pragma unroll
@@ -268,7 +277,6 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   }
 
   // T1: sum_{l >= s} CB[l, s] e^{S_l - S_s} G_l
-  const float s_row = row < lim ? sq[row] : 0.f;
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
     const int l0 = lt * 64 + st * KST;
