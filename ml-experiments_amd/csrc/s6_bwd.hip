@@ -72,14 +72,14 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
       (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3] + s0) * EB;
   const uint32_t Cst = (uint32_t)(p.sC[3] * EB);
 
-  float on[TB], dn[TB], zn[TB];
+  uint32_t on[TB], dn[TB], zn[TB];  // raw bits of the next block's inputs, in flight
   auto fetch = [&](int tb) {
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
       const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
-      on[i] = Buf<Tio>::load(rs_o, vo_o, r * st_o);
-      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
-      if (HAS_Z) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
+      on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
+      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
+      if (HAS_Z) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
     }
   };
   const int tlast = t0 + ((t1 - 1 - t0) / TB) * TB;  // first step of the last block
@@ -88,17 +88,19 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   cnx.template load<GS>(Cbase + (uint32_t)(t1 - 1 - t0) * Cst);
   float ssum = 0.f;
   bool seen_start = false;  // a sequence starts inside this chunk
+  SeqCursorRev rc{0, -1};
+  if (varlen) rc = seq_cursor_rev_at(p.cu, p.nseq, t1);
 
   for (int tb = tlast; tb >= t0; tb -= TB) {
     float oc[TB], dc[TB], zc[TB];
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-      oc[i] = on[i];
-      dc[i] = dn[i];
-      zc[i] = HAS_Z ? zn[i] : 0.f;
+      oc[i] = Buf<Tio>::from_raw(on[i]);
+      dc[i] = Buf<Tio>::from_raw(dn[i]);
+      zc[i] = HAS_Z ? Buf<Tio>::from_raw(zn[i]) : 0.f;
     }
     if (tb > t0) fetch(tb - TB);
-    const uint32_t smask = varlen ? start_mask(p.cu, p.nseq, tb, min(tb + TB, t1)) : 0u;
+    const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, tb) : 0u;
     seen_start = seen_start || smask != 0u;
 #pragma unroll
     for (int i = TB - 1; i >= 0; --i) {
@@ -249,27 +251,34 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
 
   // Per-segment inputs, double-buffered: the next (earlier) segment's loads are in flight
   // while the current one computes.
-  float un[SEG], dn[SEG], on[SEG], zn[SEG], yn[SEG], hn[NS];
+  // u / delta / dout (z, out) stay raw bits until the segment that uses them; the checkpoint
+  // row is loaded unconditionally from an in-bounds row (row 0 for the first segment, the
+  // group's last real state for padded ones) and masked at use, so no load waits or branches
+  // in the prefetch.
+  uint32_t un[SEG], dn[SEG], on[SEG], zn[SEG], yn[SEG];
+  float hn[NS];
   auto fetch = [&](int ts) {
     const int te = min(ts + SEG, t1);
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
       const uint32_t r = (uint32_t)(min(ts + i, te - 1) - t0);
-      un[i] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
-      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
-      on[i] = Buf<Tio>::load(rs_o, vo_o, r * st_o);
+      un[i] = Buf<Tio>::load_raw(rs_u, vo_u, r * st_u);
+      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
+      on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
       if (HAS_Z) {
-        zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
-        yn[i] = Buf<Tio>::load(rs_y, vo_y, r * st_y);
+        zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
+        yn[i] = Buf<Tio>::load_raw(rs_y, vo_y, r * st_y);
       }
     }
-    // state after step ts - 1 (zero at the start of the input)
-    const float* xc = xck + (int64_t)(ts / SEG - 1) * xck_step;
+    // the state after step ts - 1 (used only for ts > 0: zero at the start of the input)
+    const float* xc = xck + (int64_t)(ts > 0 ? ts / SEG - 1 : 0) * xck_step;
 #pragma unroll
-    for (int n = 0; n < NS; ++n) hn[n] = (ts > 0 && n < N) ? xc[n] : 0.f;
+    for (int n = 0; n < NS; ++n) hn[n] = xc[n < N ? n : N - 1];
   };
   const int nseg = (t1 - t0 + SEG - 1) / SEG;
   fetch(t0 + (nseg - 1) * SEG);
+  SeqCursorRev rc{0, -1};  // segments are visited from the last one down
+  if (varlen) rc = seq_cursor_rev_at(p.cu, p.nseq, t1);
 
   // Scalar-cache pipeline over half rows (HS states) of B / C, as in the forward (touch /
   // opaque, s6_common.h): consume the half row(s) in flight, issue the next, compute.
@@ -287,25 +296,27 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     float uu[SEG], dt[SEG], dy[SEG], pre[SEG], hst[NS];
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
-      uu[i] = un[i];
-      pre[i] = dn[i] + bias;
-      dt[i] = prep_dt<DTM>(dn[i], bias);
-      dy[i] = on[i];
+      const float dl = Buf<Tio>::from_raw(dn[i]), oo = Buf<Tio>::from_raw(on[i]);
+      uu[i] = Buf<Tio>::from_raw(un[i]);
+      pre[i] = dl + bias;
+      dt[i] = prep_dt<DTM>(dl, bias);
+      dy[i] = oo;
       if (HAS_Z) {
         // out_z = out * silu(z):  dy = dout silu(z),  dz = dout out sig (1 + z (1 - sig))
-        const float zz = zn[i], sg = sigmoidf_(zz);
-        dy[i] = on[i] * (zz * sg);
+        const float zz = Buf<Tio>::from_raw(zn[i]), yy = Buf<Tio>::from_raw(yn[i]);
+        const float sg = sigmoidf_(zz);
+        dy[i] = oo * (zz * sg);
         if (ts + i < te && gn == 0) {
           Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz,
-                          on[i] * yn[i] * sg * (1.f + zz * (1.f - sg)));
-          if (want_oz) Buf<Tio>::store(rs_oz, vo_oz, (uint32_t)(ts + i - t0) * st_oz, yn[i] * (zz * sg));
+                          oo * yy * sg * (1.f + zz * (1.f - sg)));
+          if (want_oz) Buf<Tio>::store(rs_oz, vo_oz, (uint32_t)(ts + i - t0) * st_oz, yy * (zz * sg));
         }
       }
     }
 #pragma unroll
-    for (int n = 0; n < NS; ++n) hst[n] = hn[n];
+    for (int n = 0; n < NS; ++n) hst[n] = (ts > 0 && n < N) ? hn[n] : 0.f;
     if (s > 0) fetch(ts - SEG);
-    const uint32_t smask = varlen ? start_mask(p.cu, p.nseq, ts, te) : 0u;
+    const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, ts) : 0u;
     float s1[SEG], s2[SEG];
 #pragma unroll
     for (int i = 0; i < SEG; ++i) s1[i] = s2[i] = 0.f;

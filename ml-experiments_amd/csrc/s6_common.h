@@ -59,11 +59,18 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
                                            0x00020000);
 }
 
+// load_raw / from_raw: a prefetched value carried into a later loop iteration stays as its
+// raw bits until used.  Converted right after its load (as load() does), it would make the
+// prefetch wait for the load in the iteration that issues it.
 template <typename T> struct Buf;
 template <> struct Buf<float> {
   __device__ static inline float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0));
   }
+  __device__ static inline uint32_t load_raw(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0);
+  }
+  __device__ static inline float from_raw(uint32_t x) { return __uint_as_float(x); }
   __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)vo, (int)so, 0);
   }
@@ -73,6 +80,10 @@ template <> struct Buf<bf16> {
     const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
     return __uint_as_float(b << 16);
   }
+  __device__ static inline uint32_t load_raw(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
+  }
+  __device__ static inline float from_raw(uint32_t x) { return __uint_as_float(x << 16); }
   __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
     const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
     __builtin_amdgcn_raw_buffer_store_b16(b, r, (int)vo, (int)so, 0);
@@ -82,6 +93,12 @@ template <> struct Buf<f16> {
   __device__ static inline float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
     const uint16_t b = __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
     return (float)__builtin_bit_cast(_Float16, b);
+  }
+  __device__ static inline uint32_t load_raw(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0);
+  }
+  __device__ static inline float from_raw(uint32_t x) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
   }
   __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
     const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));

@@ -121,16 +121,16 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   float ssum = 0.f;         // sum of Delta since the last sequence start (chunk summary only)
   bool seen_start = false;  // a sequence started inside this chunk
 
-  // Register double buffer: the next block's u / delta / z are in flight while the
-  // current block computes.  Loads past t1 re-read step t1 - 1.
-  float un[TB], dn[TB], zn[TB];
+  // Register double buffer: the next block's u / delta / z are in flight, as raw bits, while
+  // the current block computes.  Loads past t1 re-read step t1 - 1.
+  uint32_t un[TB], dn[TB], zn[TB];
   auto fetch = [&](int tb) {
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
       const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
-      un[i] = Buf<Tio>::load(rs_u, vo_u, r * st_u);
-      dn[i] = Buf<Tio>::load(rs_d, vo_d, r * st_d);
-      if (HAS_Z && !MULTI) zn[i] = Buf<Tio>::load(rs_z, vo_z, r * st_z);
+      un[i] = Buf<Tio>::load_raw(rs_u, vo_u, r * st_u);
+      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
+      if (HAS_Z && !MULTI) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
     }
   };
   fetch(t0);
@@ -145,9 +145,9 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     float uc[TB], dc[TB], zc[TB];
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-      uc[i] = un[i];
-      dc[i] = dn[i];
-      zc[i] = (HAS_Z && !MULTI) ? zn[i] : 0.f;
+      uc[i] = Buf<Tio>::from_raw(un[i]);
+      dc[i] = Buf<Tio>::from_raw(dn[i]);
+      zc[i] = (HAS_Z && !MULTI) ? Buf<Tio>::from_raw(zn[i]) : 0.f;
     }
     // MULTI output pass: u (and z) of the steps this wave finishes after the block,
     // i = gn + k nsg, reloaded now (they are in cache from the prefetch) so that the block's

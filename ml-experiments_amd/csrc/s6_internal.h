@@ -43,6 +43,37 @@ __device__ inline uint32_t start_mask(const int32_t* cu, int32_t nseq, int64_t t
   return m;
 }
 
+// Reverse cursor for kernels that visit [t0, t1) in consecutive decreasing ranges: pend is the
+// largest sequence start below the ranges still to visit (-1 when there is none), hi - 1 its
+// index in cu_seqlens.  start_mask_rev then costs one compare per range and one load per
+// start passed, where start_mask searches cu_seqlens again for every range.
+struct SeqCursorRev {
+  int32_t hi;
+  int64_t pend;
+};
+
+__device__ inline SeqCursorRev seq_cursor_rev_at(const int32_t* cu, int32_t nseq, int64_t t1) {
+  const SeqCursor s = seq_cursor_at(cu, nseq, t1);  // first i with cu[i] >= t1
+  SeqCursorRev r;
+  r.hi = s.idx;
+  r.pend = s.idx > 0 ? (int64_t)cu[s.idx - 1] : -1;
+  return r;
+}
+
+// The bits start_mask(cu, nseq, ts, te) sets, for te = the previous call's ts (the first call:
+// seq_cursor_rev_at's t1); offsets past 31 set no bit.  Every iteration lowers hi, so the loop
+// ends for any vector.
+__device__ inline uint32_t start_mask_rev(SeqCursorRev& r, const int32_t* cu, int64_t ts) {
+  uint32_t m = 0;
+  while (r.hi > 0 && r.pend >= ts) {
+    const int64_t off = r.pend - ts;
+    if (off < 32) m |= 1u << (uint32_t)off;
+    --r.hi;
+    r.pend = r.hi > 0 ? (int64_t)cu[r.hi - 1] : -1;
+  }
+  return m;
+}
+
 // Stores the first N (<= NS) states of one lane to a contiguous fp32 row.
 template <int NS>
 __device__ inline void store_state(float* dst, const float (&h)[NS], int N) {

@@ -262,11 +262,12 @@ def test_backward_contiguous_layout():
 
 
 @pytest.mark.parametrize("zb", [True, False], ids=["z_softplus", "plain"])
-@pytest.mark.parametrize("cu", [[0, 100, 101, 450, 700, 1000], [0, 32, 64, 96, 1000], [0, 1000]])
+@pytest.mark.parametrize("cu", [[0, 100, 101, 450, 700, 1000], [0, 32, 64, 96, 1000], [0, 1000],
+                                [0, 3, 5, 6, 7, 300, 1000]])
 def test_varlen_forward_and_backward(cu, zb):
-    """Sequence starts inside segments, on segment boundaries and at single-step sequences,
-    for the z-gated softplus backward and the plain one (they keep different values in LDS
-    between the recompute and the reverse sweep)."""
+    """Sequence starts inside segments, on segment boundaries, at single-step sequences and
+    four in one 8-step segment, for the z-gated softplus backward and the plain one (they
+    keep different values in LDS between the recompute and the reverse sweep)."""
     inp = gen(1, 1000, 64, 16, torch.float32, seed=11, z=zb, bias=zb)
     cu = torch.tensor(cu, dtype=torch.int32)
     out_ref, ls_ref = ref_fwd(inp, cu)
