@@ -15,13 +15,20 @@ namespace s6 {
 //   REV:     ws[ch, c] = gradient chunk c passes out of its first step from a zero inflow
 //            -> gradient flowing into chunk c from chunk c + 1
 // The chunk composed last (forward: c = K-1; REV: c = 0) has no summary of its own.
-template <bool REV>
+// The group's loads are unconditional, from chunk min(step, K - 2) (in bounds), and the steps
+// past K - 2 are masked at use: a load under a branch (as `has ? ws[..] : 0` compiles to)
+// waits for itself before the branch joins, one round trip per chunk.
+template <bool REV, bool VARLEN>
 __global__ void __launch_bounds__(256) chunk_carry(CarryK p) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= p.nch * p.N) return;
   const int64_t ch = i / p.N, n = i % p.N;
   const int64_t d = ch % p.D;
   const int64_t K = p.K;
+  if (K < 2) {  // one chunk: nothing flows into it
+    p.ws[ch * K * p.N + n] = 0.f;
+    return;
+  }
   const float ap = p.A[d * p.sA[0] + n * p.sA[1]] * kLog2e;
   constexpr int G = 16;
   float carry = 0.f;
@@ -30,12 +37,11 @@ __global__ void __launch_bounds__(256) chunk_carry(CarryK p) {
     int rs[G];
 #pragma unroll
     for (int k = 0; k < G; ++k) {
-      const int64_t step = s0 + k;
+      const int64_t step = min(s0 + k, K - 2);
       const int64_t c = REV ? K - 1 - step : step;
-      const bool has = step < K - 1;  // every chunk but the one composed last
-      hl[k] = has ? p.ws[(ch * K + c) * p.N + n] : 0.f;
-      S[k] = has ? p.ws_s[ch * K + c] : 0.f;
-      rs[k] = (has && p.ws_r != nullptr) ? p.ws_r[ch * K + c] : 0;
+      hl[k] = p.ws[(ch * K + c) * p.N + n];
+      S[k] = p.ws_s[ch * K + c];
+      rs[k] = VARLEN ? p.ws_r[ch * K + c] : 0;
     }
 #pragma unroll
     for (int k = 0; k < G; ++k) {
@@ -177,7 +183,11 @@ static unsigned grid_for(int64_t total, int64_t threads) {
 template <bool REV>
 static hipError_t launch_carry(const CarryK& c, hipStream_t st) {
   const int64_t total = c.nch * c.N;
-  hipLaunchKernelGGL((chunk_carry<REV>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, c);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (c.ws_r != nullptr)
+    hipLaunchKernelGGL((chunk_carry<REV, true>), grid, dim3(256), 0, st, c);
+  else
+    hipLaunchKernelGGL((chunk_carry<REV, false>), grid, dim3(256), 0, st, c);
   return hipGetLastError();
 }
 
