@@ -52,13 +52,18 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   const int N = (int)p.N - s0;                   // states of the group (may exceed NS)
   const bool varlen = p.nseq > 0;
 
+  // Prologue loads unconditional from in-bounds addresses, masked afterwards (a load under a
+  // branch waits for itself before the branch joins).
   float Ap[NS], gs[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
+    const float a = p.A[d * p.sA[0] + (s0 + (n < N ? n : N - 1)) * p.sA[1]];
+    Ap[n] = (n < N) ? a * kLog2e : 0.f;
     gs[n] = 0.f;
   }
-  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
+  const bool hb = DTM != kDtRaw && p.has_bias;
+  const float bias_v = (hb ? p.bias : p.A)[hb ? d * p.sbias : 0];
+  const float bias = hb ? bias_v : 0.f;
   const auto rs_o = make_rsrc((const char*)p.dout + (b * p.sdo[0] + d0 * p.sdo[1] + (int64_t)t0 * p.sdo[2]) * ES);
   const auto rs_d = make_rsrc((const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1] + (int64_t)t0 * p.sdl[2]) * ES);
   const auto rs_z = make_rsrc(HAS_Z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1] + (int64_t)t0 * p.sz[2]) * ES
@@ -183,16 +188,24 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
 
   float Ap[NS], gs[NS], dAacc[NS];
   {
-    const float* gin = p.ws_g + (ch * p.K + c) * p.N + s0;
+    // prologue loads unconditional from in-bounds addresses, masked afterwards (a load under
+    // a branch waits for itself before the branch joins); the carried gradient exists for K > 1
+    const float* gin = p.K > 1 ? p.ws_g + (ch * p.K + c) * p.N + s0 : p.A;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
-      Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
-      gs[n] = (n < N && p.K > 1) ? gin[n] : 0.f;
+      const int nc = n < N ? n : N - 1;
+      const float a = p.A[d * p.sA[0] + (s0 + nc) * p.sA[1]];
+      const float gv = gin[p.K > 1 ? nc : 0];
+      Ap[n] = (n < N) ? a * kLog2e : 0.f;
+      gs[n] = (n < N && p.K > 1) ? gv : 0.f;
       dAacc[n] = 0.f;
     }
   }
-  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
-  const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
+  const bool hb = DTM != kDtRaw && p.has_bias;
+  const float bias_v = (hb ? p.bias : p.A)[hb ? d * p.sbias : 0];
+  const float bias = hb ? bias_v : 0.f;
+  const float Dv_v = (p.has_D ? p.Dp : p.A)[p.has_D ? d * p.sD : 0];
+  const float Dv = p.has_D ? Dv_v : 0.f;
   float dDacc = 0.f, dbacc = 0.f;
 
   // Buffer resources based at (b, d0, t0); inactive lanes load 0 and drop their stores.

@@ -73,19 +73,30 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
 
   float Ap[NS];
   float h[NS];
+  // Prologue loads are unconditional, from in-bounds addresses (the group's last real state
+  // for padded ones, A in place of an absent bias / D), and masked afterwards: a load under a
+  // branch waits for itself before the branch joins, one round trip each.
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    Ap[n] = (n < N) ? p.A[d * p.sA[0] + (s0 + n) * p.sA[1]] * kLog2e : 0.f;
+    const float a = p.A[d * p.sA[0] + (s0 + (n < N ? n : N - 1)) * p.sA[1]];
+    Ap[n] = (n < N) ? a * kLog2e : 0.f;
     h[n] = 0.f;
   }
   const int64_t ch = b * p.D + d;  // channel index for workspaces
   if (FULL && c > 0) {
     const float* hin = p.ws_h + (ch * p.K + c) * p.N + s0;
 #pragma unroll
-    for (int n = 0; n < NS; ++n) h[n] = (n < N) ? hin[n] : 0.f;
+    for (int n = 0; n < NS; ++n) {
+      const float v = hin[n < N ? n : N - 1];
+      h[n] = (n < N) ? v : 0.f;
+    }
   }
-  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
-  const float Dv = (FULL && p.has_D) ? p.Dp[d * p.sD] : 0.f;
+  const bool hb = DTM != kDtRaw && p.has_bias;
+  const float bias_v = (hb ? p.bias : p.A)[hb ? d * p.sbias : 0];
+  const float bias = hb ? bias_v : 0.f;
+  const bool hd = FULL && p.has_D;
+  const float Dv_v = (hd ? p.Dp : p.A)[hd ? d * p.sD : 0];
+  const float Dv = hd ? Dv_v : 0.f;
   // checkpoints: [batch, nck, dim, dstate]
   float* const xck = (FULL && p.x_ckpt != nullptr) ? p.x_ckpt + b * p.sck[0] + d * p.sck[2] + s0 : nullptr;
   const int64_t xck_step = p.sck[1];

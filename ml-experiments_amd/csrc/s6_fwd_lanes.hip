@@ -178,9 +178,15 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   const bool live = s < N;
   const int L = (int)p.L;
 
-  const float Ap = live ? p.A[d * p.sA[0] + s * p.sA[1]] * kLog2e : 0.f;
-  const float bias = (DTM != kDtRaw && p.has_bias) ? p.bias[d * p.sbias] : 0.f;
-  const float Dv = p.has_D ? p.Dp[d * p.sD] : 0.f;
+  // unconditional loads from in-bounds addresses (A in place of an absent bias / D), masked
+  // afterwards: a load under a branch waits for itself before the branch joins
+  const float a_v = p.A[d * p.sA[0] + (live ? s : N - 1) * p.sA[1]];
+  const float Ap = live ? a_v * kLog2e : 0.f;
+  const bool hb = DTM != kDtRaw && p.has_bias;
+  const float bias_v = (hb ? p.bias : p.A)[hb ? d * p.sbias : 0];
+  const float bias = hb ? bias_v : 0.f;
+  const float Dv_v = (p.has_D ? p.Dp : p.A)[p.has_D ? d * p.sD : 0];
+  const float Dv = p.has_D ? Dv_v : 0.f;
 
   // Buffer addressing (s6_common.h): a wave-uniform base rebuilt per block and 32-bit lane
   // offsets; lanes given kOffDrop read zeros and drop their stores, so no store needs a
