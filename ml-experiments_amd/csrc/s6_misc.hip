@@ -69,14 +69,35 @@ __global__ void __launch_bounds__(256) bwd_reduce_bc(BwdK p) {
       float sb[W], sc[W];
 #pragma unroll
       for (int n = 0; n < W; ++n) sb[n] = sc[n] = 0.f;
-      for (int64_t j = 0; j < p.nJ; ++j) {
-        const int64_t row = ((bg * p.nJ + j) * p.L + t) * p.NPr + n0;
+      // Rows in groups of RG: the group's loads are issued together (in flight at once), then
+      // added in row order j = 0, 1, ... (the result does not depend on the grouping).
+      constexpr int RG = 4;
+      for (int64_t j0 = 0; j0 < p.nJ; j0 += RG) {
+        float4 vb[RG][W / 4], vc[RG][W / 4];
 #pragma unroll
-        for (int n = 0; n < W; n += 4) {
-          const float4 vb = *reinterpret_cast<const float4*>(p.ws_pB + row + n);
-          const float4 vc = *reinterpret_cast<const float4*>(p.ws_pC + row + n);
-          sb[n] += vb.x; sb[n + 1] += vb.y; sb[n + 2] += vb.z; sb[n + 3] += vb.w;
-          sc[n] += vc.x; sc[n + 1] += vc.y; sc[n + 2] += vc.z; sc[n + 3] += vc.w;
+        for (int r = 0; r < RG; ++r) {
+          const int64_t j = min(j0 + r, p.nJ - 1);  // in bounds; rows past nJ are not added
+          const int64_t row = ((bg * p.nJ + j) * p.L + t) * p.NPr + n0;
+#pragma unroll
+          for (int q = 0; q < W / 4; ++q) {
+            vb[r][q] = *reinterpret_cast<const float4*>(p.ws_pB + row + 4 * q);
+            vc[r][q] = *reinterpret_cast<const float4*>(p.ws_pC + row + 4 * q);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          // rows past nJ add an exact 0 (a select, not a branch, which would let the compiler
+          // sink the group's loads behind each other)
+          const bool on = j0 + r < p.nJ;
+#pragma unroll
+          for (int q = 0; q < W / 4; ++q) {
+            const int n = 4 * q;
+            const float4 b4 = vb[r][q], c4 = vc[r][q];
+            sb[n] += on ? b4.x : 0.f; sb[n + 1] += on ? b4.y : 0.f;
+            sb[n + 2] += on ? b4.z : 0.f; sb[n + 3] += on ? b4.w : 0.f;
+            sc[n] += on ? c4.x : 0.f; sc[n + 1] += on ? c4.y : 0.f;
+            sc[n + 2] += on ? c4.z : 0.f; sc[n + 3] += on ? c4.w : 0.f;
+          }
         }
       }
 #pragma unroll
