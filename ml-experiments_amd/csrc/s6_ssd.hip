@@ -362,11 +362,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bmm(SsdK k) {
   for (int i = 0; i < 4; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int n0 = 0; n0 < N; n0 += kKs) {
-    const typename M::Frag a = row < lim ? M::load_row(Cb + row * k.sC[1] + n0, lane) : M::zero();
+    // rows / columns past lim read the last valid row; their CB entries are zeroed below
+    const typename M::Frag a = M::load_row(Cb + min(row, lim - 1) * k.sC[1] + n0, lane);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const int s = tj * 64 + 16 * ct + (lane & 15);
-      const typename M::Frag bf = s < lim ? M::load_row(Bb + s * k.sB[1] + n0, lane) : M::zero();
+      const typename M::Frag bf = M::load_row(Bb + min(s, lim - 1) * k.sB[1] + n0, lane);
       M::mma(acc[ct], a, bf);
     }
   }
@@ -378,7 +379,8 @@ __global__ void __launch_bounds__(kThreads) ssd_bmm(SsdK k) {
       const int l = ti * 64 + 16 * w + 4 * (lane >> 4) + j;
       const int s = tj * 64 + 16 * ct + (lane & 15);
       float v = acc[ct][j];
-      if (k.has_seq && l < lim && s < lim && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
+      if (!(l < lim && s < lim)) v = 0.f;
+      else if (k.has_seq && seq_at(k, b, t0 + l) != seq_at(k, b, t0 + s)) v = 0.f;
       out[(int64_t)l * k.Q + s] = v;
     }
   }
@@ -483,13 +485,12 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   fetch(0);
   // Values used only after the state term: loaded here, with the first stage, so that no
   // later step waits a full memory latency for them.
-  const float s_row = row < lim ? sq[row] : 0.f;  // S of this lane's A-operand row
-  float s_acc[4];                                  // S of this lane's accumulator rows
+  // Rows < Q are in bounds; rows past lim are masked where these are used.  Loaded without a
+  // condition: a conditional load would wait for itself under its branch.
+  const float s_row = sq[row];  // S of this lane's A-operand row
+  float s_acc[4];               // S of this lane's accumulator rows
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int l = rowbase + 4 * (lane >> 4) + j;
-    s_acc[j] = l < lim ? sq[l] : 0.f;
-  }
+  for (int j = 0; j < 4; ++j) s_acc[j] = sq[rowbase + 4 * (lane >> 4) + j];
   const float D_head = (k.has_D && !k.D_hdim) ? k.Dp[hh * k.sD[0]] : 0.f;
 
   f4 acc[PT];
@@ -501,7 +502,8 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
   // loads; each wave's C fragments come straight from global memory.  The condition is
   // block-uniform, so the barriers inside are too.
   if (c > 0 || k.has_init) {
-    const Raw* Crow = (const Raw*)k.Cm + b * k.sC[0] + (t0 + row) * k.sC[1] + g * k.sC[2];
+    // rows past lim read the last valid row: their outputs are scaled by f = 0 below
+    const Raw* Crow = (const Raw*)k.Cm + b * k.sC[0] + (t0 + min(row, lim - 1)) * k.sC[1] + g * k.sC[2];
     const Raw* H = (const Raw*)k.hs + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
     constexpr int HC = P * (HCH / VE);
     constexpr int HL = (HC + kThreads - 1) / kThreads;
@@ -509,7 +511,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan(SsdK k) {
     for (int nc = 0; nc < N; nc += HCH) {
       typename M::Frag af[HCH / kKs];
 #pragma unroll
-      for (int i = 0; i < HCH / kKs; ++i) af[i] = row < lim ? M::load_row(Crow + nc + i * kKs, lane) : M::zero();
+      for (int i = 0; i < HCH / kKs; ++i) af[i] = M::load_row(Crow + nc + i * kKs, lane);
       u4 hv[HL];
 #pragma unroll
       for (int i = 0; i < HL; ++i) {

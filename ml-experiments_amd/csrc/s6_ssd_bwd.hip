@@ -202,14 +202,15 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
 #pragma unroll
         for (int q = 0; q < VE; ++q) gv[i][q] = M::to_raw(0.f);
     }
-    if (tid < KST) sv = l0 + tid < k.Q ? sq[l0 + tid] : 0.f;
+    // in bounds for any l0; steps past the chunk are masked where the value is used (on)
+    if (tid < KST) sv = sq[min(l0 + tid, (int)k.Q - 1)];
 #pragma unroll
     for (int ks = 0; ks < SUB; ++ks) {
       const bool reach = l0 + ks * kKs + kKs - 1 >= rowbase;  // wave-uniform
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int l = l0 + ks * kKs + M::kidx(lane, j);
-        cbv[ks][j] = (reach && l < lim) ? cbcol[(int64_t)l * k.Q] : 0.f;
+        cbv[ks][j] = cbcol[(int64_t)min(l, (int)k.Q - 1) * k.Q];  // masked at use (on)
       }
     }
   };
@@ -217,13 +218,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
   // Values used only after the T2 product: loaded here, with the first stage, so that no
   // later step waits a full memory latency for them.
   const float s_last = sq[k.Q - 1];
-  const float s_row = row < lim ? sq[row] : 0.f;  // S of this lane's A-operand row
-  float s_acc[4];                                  // S of this lane's accumulator rows
+  // Rows < Q are in bounds; rows past lim are masked where these are used.  Loaded without a
+  // condition: a conditional load would wait for itself under its branch.
+  const float s_row = sq[row];  // S of this lane's A-operand row
+  float s_acc[4];               // S of this lane's accumulator rows
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int s = rowbase + 4 * (lane >> 4) + j;
-    s_acc[j] = s < lim ? sq[s] : 0.f;
-  }
+  for (int j = 0; j < 4; ++j) s_acc[j] = sq[rowbase + 4 * (lane >> 4) + j];
 
   f4 acc[PT];
 #pragma unroll
@@ -231,7 +231,8 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
 
   // T2: B_s dst^T, rows scaled by mlast e^{S_last - S_s}; dst staged through LDS
   {
-    const Raw* Brow = (const Raw*)k.Bm + b * k.sB[0] + (t0 + row) * k.sB[1] + g * k.sB[2];
+    // rows past lim read the last valid row (their outputs are scaled by 0 below)
+    const Raw* Brow = (const Raw*)k.Bm + b * k.sB[0] + (t0 + min(row, lim - 1)) * k.sB[1] + g * k.sB[2];
     const Raw* D2 = (const Raw*)k.dst + ((b * k.K + c) * k.H + hh) * (int64_t)(P * N);
     constexpr int HC = P * (HCH / VE);
     constexpr int HL = (HC + kThreads - 1) / kThreads;
@@ -239,7 +240,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dx(SsdK k) {
     for (int nc = 0; nc < N; nc += HCH) {
       typename M::Frag af[HCH / kKs];
 #pragma unroll
-      for (int i = 0; i < HCH / kKs; ++i) af[i] = row < lim ? M::load_row(Brow + nc + i * kKs, lane) : M::zero();
+      for (int i = 0; i < HCH / kKs; ++i) af[i] = M::load_row(Brow + nc + i * kKs, lane);
       u4 hv[HL];
 #pragma unroll
       for (int i = 0; i < HL; ++i) {
@@ -445,7 +446,8 @@ __global__ void __launch_bounds__(kThreads)
   const int rowbase = lt * 64 + 16 * w;
   const int row = rowbase + (lane & 15);
   const int64_t* sa = MODE == 4 ? k.sx : k.sdy;
-  const Raw* abase = (const Raw*)(MODE == 4 ? k.x : k.dy) + b * sa[0] + (t0 + row) * sa[1];
+  // A-operand rows past lim read the last valid row: their accumulator rows get f = 0
+  const Raw* abase = (const Raw*)(MODE == 4 ? k.x : k.dy) + b * sa[0] + (t0 + min(row, lim - 1)) * sa[1];
   const void* side = MODE == 4 ? k.Bm : k.Cm;
   const int64_t* ss = MODE == 4 ? k.sB : k.sC;
   const int32_t seq_ref = !k.has_seq ? 0
@@ -460,8 +462,8 @@ __global__ void __launch_bounds__(kThreads)
     rv[j] = l < lim && (!k.has_seq || seq_at(k, b, t0 + l) == seq_ref);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-      sd[j][nt] = l < lim ? Elem<T>::load(side, b * ss[0] + (t0 + l) * ss[1] + g * ss[2] + ns * NC + nt * 16 + (lane & 15))
-                          : 0.f;
+      // rows past lim read the last valid row: their terms are scaled by f = 0 (rv)
+      sd[j][nt] = Elem<T>::load(side, b * ss[0] + (t0 + min(l, lim - 1)) * ss[1] + g * ss[2] + ns * NC + nt * 16 + (lane & 15));
   }
   f4 tot[NT];
 #pragma unroll
@@ -479,13 +481,13 @@ __global__ void __launch_bounds__(kThreads)
       if (e < MC) load16<T>(mat + p * N + ns * NC + n0, mv[i]);
     }
 #pragma unroll
-    for (int kk = 0; kk < KF; ++kk) af[kk] = row < lim ? M::load_row(abase + hh * sa[2] + kk * kKs, lane) : M::zero();
+    for (int kk = 0; kk < KF; ++kk) af[kk] = M::load_row(abase + hh * sa[2] + kk * kKs, lane);
     const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j;
-      sqv[j] = l < lim ? k.dacs[hrow + l] : 0.f;
-      dqv[j] = (MODE == 4 && l < lim) ? k.dtq[hrow + l] : 0.f;
+      sqv[j] = k.dacs[hrow + l];  // l < Q: in bounds; rows past lim get f = 0 (rv)
+      dqv[j] = MODE == 4 ? k.dtq[hrow + l] : 0.f;
     }
     if (MODE == 4) slv = k.dacs[hrow + k.Q - 1];
   };
@@ -599,7 +601,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dcb(SsdK k) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j, s = J * 64 + ct * 16 + (lane & 15);
-      cbv[ct][j] = (l < lim && s < lim) ? cbm[(int64_t)l * k.Q + s] : 0.f;
+      cbv[ct][j] = cbm[(int64_t)l * k.Q + s];  // l, s < Q: in bounds; used only where on
     }
   f4 dcb[4];
 #pragma unroll
@@ -620,14 +622,15 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_dcb(SsdK k) {
 #pragma unroll
         for (int q = 0; q < VE; ++q) xv[i][q] = M::to_raw(0.f);
     }
-    const Raw* grow = (const Raw*)k.dy + b * k.sdy[0] + (t0 + row) * k.sdy[1] + hh * k.sdy[2];
+    // rows past lim read the last valid row: every dM term of such a row is masked below
+    const Raw* grow = (const Raw*)k.dy + b * k.sdy[0] + (t0 + min(row, lim - 1)) * k.sdy[1] + hh * k.sdy[2];
 #pragma unroll
-    for (int kk = 0; kk < KF; ++kk) gf[kk] = row < lim ? M::load_row(grow + kk * kKs, lane) : M::zero();
+    for (int kk = 0; kk < KF; ++kk) gf[kk] = M::load_row(grow + kk * kKs, lane);
     const int64_t hrow = ((b * k.H + hh) * k.K + c) * k.Q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int l = rowbase + 4 * (lane >> 4) + j;
-      slv[j] = l < lim ? k.dacs[hrow + l] : 0.f;
+      slv[j] = k.dacs[hrow + l];  // l < Q: in bounds; used only where on
     }
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
