@@ -57,6 +57,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fwdbwd", action="store_true",
                     help="fwd1 only: skip the config-3 fwd+bwd measurement carried in its line")
+    ap.add_argument("--layout", default="channel_last", choices=["channel_last", "l_contiguous"],
+                    help="scan workloads: [B, D, L] arguments as channel-last views of [B, L, D] "
+                         "tensors (default), or L-contiguous tensors as the reference's zoology "
+                         "Mamba passes them")
     return ap.parse_args()
 
 
@@ -566,9 +570,12 @@ def copy_reference(torch, steps):
                       "bytes_written_per_launch": 4 * n, "launches": max(steps, 1)}))
 
 
-def measure_scan(torch, workload, steps, warmup):
+def measure_scan(torch, workload, steps, warmup, layout="channel_last"):
     """One of the scan workloads (fwd1, fwdbwd3, fwd2, fwdbwd4, mixer1): its bench dict,
-    without the CPU baseline."""
+    without the CPU baseline.  ``layout`` "l_contiguous" stores every [B, L, *] input as
+    [B, *, L] (same shape, time axis contiguous), so that the [B, *, L] arguments the steps
+    pass (``.mT``) are L-contiguous, as zoology's Mamba passes them (mamba.py:128-132,
+    176-179)."""
     import ctypes
 
     from s6scan import _lib
@@ -590,6 +597,8 @@ def measure_scan(torch, workload, steps, warmup):
         st = {k: v.to(dev) for k, v in cpu.items()}
         if mixer:
             st.update(mixer_extras(torch, st, torch.Generator("cpu").manual_seed(77 + s)))
+        if layout == "l_contiguous":
+            st = {k: (v.mT.contiguous().mT if v.dim() == 3 else v) for k, v in st.items()}
         sets.append(st)
         del cpu
     L = sets[0]["x"].shape[1]
@@ -676,7 +685,7 @@ def measure_scan(torch, workload, steps, warmup):
     traffic = valu_busy = fwd_traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            prof = json.load(f).get(workload)
+            prof = json.load(f).get(workload if layout == "channel_last" else workload + "_lc")
         if prof:
             traffic = round(prof["traffic_bytes_per_launch"])
             valu_busy = round(prof["kernels"][prof["dominant_kernel"]]["valu_busy"], 3)
@@ -703,7 +712,10 @@ def measure_scan(torch, workload, steps, warmup):
                                 "B/C slices of x_proj output)" if mixer else
                                 f"{cfg.name}: s6scan selective_scan_forward"
                                 f"{' + selective_scan_backward' if cfg.backward else ''} (the "
-                                "launches selective_scan_fn makes) on channel-last [B, L, D] views"),
+                                "launches selective_scan_fn makes) on "
+                                + ("channel-last [B, L, D] views" if layout == "channel_last"
+                                   else "[B, D, L] L-contiguous tensors")),
+                   "layout": layout,
                    "forward_kernel": fwd_kernel,
                    "batch": B, "seqlen": L, "dim": cfg.dim, "dstate": cfg.dstate,
                    "nseq": cfg.nseq, "algorithmic_bytes_per_step": nbytes},
@@ -773,12 +785,13 @@ def main():
     if args.workload == "ssd2":
         run_ssd(torch, args)
         return
-    res = measure_scan(torch, args.workload, args.steps, args.warmup)
+    res = measure_scan(torch, args.workload, args.steps, args.warmup, args.layout)
     if args.workload == "fwd1" and not args.no_fwdbwd:
         # BASELINE's metric covers fwd and fwd+bwd: the training-shape fwd+bwd (config 3)
         # rides along, measured the same way; value stays the config-1 forward.
         log("fwd+bwd (config 3) ...")
-        fb = measure_scan(torch, "fwdbwd3", max(10, args.steps // 2), max(3, args.warmup // 2))
+        fb = measure_scan(torch, "fwdbwd3", max(10, args.steps // 2), max(3, args.warmup // 2),
+                          args.layout)
         res["fwd_bwd"] = {k: fb[k] for k in ("value", "unit", "ms_per_step", "hbm_frac",
                                               "mtok_ch_per_s", "steps", "config", "roofline",
                                               "fwd_kernel_ms", "whole_forward",

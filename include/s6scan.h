@@ -162,6 +162,15 @@ int s6_validate_cu_seqlens(const int32_t* cu_host, int64_t nseq, int64_t seqlen)
  * timing or profiling. */
 int s6_fwd_single_pass(const S6Problem* p);
 
+/* Host-only: 1 if the chunked forward moves these arguments' u / delta / z / out / out_z in
+ * whole blocks of 8 steps per lane (16-byte accesses: each of those tensors has a contiguous
+ * time axis, 16-byte aligned rows and blocks, seqlen is a multiple of 8 and dstate <= 32),
+ * 0 if one step at a time (any strides) or on the single-pass kernel, or a negative code for
+ * invalid arguments (the workspace is not checked).  Follows the environment override
+ * S6_FWD_ROWVEC=0 (per-step accesses) as s6_fwd does.  Both give bit-identical results.  No
+ * counterpart in the reference: it names the kernel variant a caller is timing. */
+int s6_fwd_row_blocks(const S6FwdArgs* a);
+
 /* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */
 int64_t s6_num_checkpoints(const S6Problem* p);
 

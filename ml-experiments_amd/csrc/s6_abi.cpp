@@ -281,6 +281,27 @@ void ckpt_strides(const int64_t* given, const S6Problem& p, int64_t nck, int64_t
   }
 }
 
+// Whole 8-step row blocks in the chunked forward (Row8 in s6_common.h): the tensor's time
+// axis is contiguous and every block of 8 steps of every row starts 16-byte aligned (the
+// chunk length is a multiple of 8, so whole blocks when the sequence length is too).
+bool rows_vec_ok(const void* ptr, const int64_t s[3], int es, const S6Problem& p) {
+  if (s[2] != 1 || ((uintptr_t)ptr & 15u) != 0) return false;
+  return (p.batch == 1 || (s[0] * es) % 16 == 0) && (p.dim == 1 || (s[1] * es) % 16 == 0);
+}
+
+// S6_FWD_ROWVEC=0 in the environment keeps the per-step loads and stores (for measurement).
+bool choose_rowvec(const S6FwdArgs& a, const Plan& pl) {
+  const S6Problem& p = a.p;
+  if (pl.lanes || p.dstate > 32 || p.seqlen % s6::kCk != 0) return false;
+  const char* env = getenv("S6_FWD_ROWVEC");
+  if (env != nullptr && strcmp(env, "0") == 0) return false;
+  const int es = esize(p.io_dtype);
+  bool ok = rows_vec_ok(a.u, a.u_stride, es, p) && rows_vec_ok(a.delta, a.delta_stride, es, p) &&
+            rows_vec_ok(a.out, a.out_stride, es, p);
+  if (p.has_z) ok = ok && rows_vec_ok(a.z, a.z_stride, es, p) && rows_vec_ok(a.out_z, a.out_z_stride, es, p);
+  return ok;
+}
+
 s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   s6::FwdK k{};
   const S6Problem& p = a.p;
@@ -322,6 +343,7 @@ s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   k.nDblk = pl.nDblk;
   k.nsg = (int32_t)nsg_fwd(p.dstate);
   k.lanes = pl.lanes ? 1 : 0;
+  k.rowvec = choose_rowvec(a, pl) ? 1 : 0;
   return k;
 }
 
@@ -1057,6 +1079,13 @@ size_t s6_bwd_workspace_bytes(const S6Problem* p) {
 }
 
 int s6_validate_fwd(const S6FwdArgs* a) { return validate_fwd(a, true); }
+
+int s6_fwd_row_blocks(const S6FwdArgs* a) {
+  int r = validate_fwd(a, false);
+  if (r != S6_OK) return r;
+  const Plan pl = make_plan(a->p, false, a->B, a->B_stride, a->C, a->C_stride);
+  return choose_rowvec(*a, pl) ? 1 : 0;
+}
 
 }  // extern "C"
 

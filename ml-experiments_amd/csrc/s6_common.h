@@ -43,6 +43,7 @@ template <> struct Elem<f16> {
     return static_cast<float>(reinterpret_cast<const _Float16*>(p)[i]);
   }
   __device__ static inline void store(void* p, int64_t i, float v) {
+    asm("" : "+v"(v));  // rounded to fp32 first (see Buf<f16>::store)
     reinterpret_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
   }
 };
@@ -100,9 +101,88 @@ template <> struct Buf<f16> {
   __device__ static inline float from_raw(uint32_t x) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
   }
+  // The value is rounded to fp32 first, as the reference converts its fp32 results: the
+  // empty asm stops the compiler from fusing a producing fma into v_fma_mixlo_f16, which
+  // rounds once, straight to fp16 (one ulp apart now and then).
   __device__ static inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+    asm("" : "+v"(v));
     const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
     __builtin_amdgcn_raw_buffer_store_b16(b, r, (int)vo, (int)so, 0);
+  }
+};
+
+// Row8<T>: eight consecutive time steps of one lane's row, packed in the storage format (two
+// 16-bit values per word).  load() / store() move a whole block with 16-byte buffer accesses
+// (one for the 16-bit formats, two for fp32): for a tensor whose time axis is contiguous and
+// 16-byte aligned at every block of 8 steps, this replaces eight per-step accesses, each of
+// which touches one cache line per lane.  pack() rounds to the storage format as the
+// per-step store() does (round to nearest even), set2(k, ., .) steps 2k and 2k + 1;
+// settle() is an empty asm that reads the words, so that their load completes there.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <typename T> struct Row8;
+template <> struct Row8<float> {
+  u32x4 w[2];
+  __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, (int)so, 0);
+    w[1] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, (int)(so + 16), 0);
+  }
+  __device__ inline void settle() const { asm volatile("" ::"v"(w[0]), "v"(w[1])); }
+  __device__ inline float get(int i) const { return __uint_as_float(w[i >> 2][i & 3]); }
+  __device__ inline void set2(int k, float y0, float y1) {
+    w[k >> 1][(k & 1) * 2] = __float_as_uint(y0);
+    w[k >> 1][(k & 1) * 2 + 1] = __float_as_uint(y1);
+  }
+  __device__ inline void pack(const float (&y)[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) set2(k, y[2 * k], y[2 * k + 1]);
+  }
+  __device__ inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) const {
+    __builtin_amdgcn_raw_buffer_store_b128(w[0], r, (int)vo, (int)so, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(w[1], r, (int)vo, (int)(so + 16), 0);
+  }
+};
+template <> struct Row8<bf16> {
+  u32x4 w;
+  __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    w = __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, (int)so, 0);
+  }
+  __device__ inline void settle() const { asm volatile("" ::"v"(w)); }
+  __device__ inline float get(int i) const {
+    const uint32_t x = w[i >> 1];
+    return __uint_as_float((i & 1) ? (x & 0xffff0000u) : (x << 16));
+  }
+  __device__ inline void set2(int k, float y0, float y1) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){y0, y1}, bf16x2));
+  }
+  __device__ inline void pack(const float (&y)[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) set2(k, y[2 * k], y[2 * k + 1]);
+  }
+  __device__ inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) const {
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, (int)vo, (int)so, 0);
+  }
+};
+template <> struct Row8<f16> {
+  u32x4 w;
+  __device__ inline void load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    w = __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, (int)so, 0);
+  }
+  __device__ inline void settle() const { asm volatile("" ::"v"(w)); }
+  __device__ inline float get(int i) const {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i >> 1] >> ((i & 1) * 16)));
+  }
+  __device__ inline void set2(int k, float y0, float y1) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){y0, y1}, f16x2));
+  }
+  __device__ inline void pack(const float (&y)[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) set2(k, y[2 * k], y[2 * k + 1]);
+  }
+  __device__ inline void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) const {
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, (int)vo, (int)so, 0);
   }
 };
 
@@ -285,6 +365,7 @@ struct FwdK {
                   // G * ceil(D / G / channels per workgroup) (single-pass kernel)
   int32_t nsg;    // dstate > 32: groups of 16 states, one wave each per workgroup (<= 4)
   int32_t lanes;  // 1: single-pass kernel, one lane per (channel, state) (s6_fwd_lanes.hip)
+  int32_t rowvec; // 1: chunked kernels read and write whole 8-step row blocks (Row8)
 };
 
 }  // namespace s6

@@ -66,6 +66,7 @@ template <> __device__ inline uint32_t to_bits<bf16>(float v) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
 template <> __device__ inline uint32_t to_bits<f16>(float v) {
+  asm("" : "+v"(v));  // rounded to fp32 first (see Buf<f16>::store)
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 

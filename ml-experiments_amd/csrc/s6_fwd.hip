@@ -33,7 +33,13 @@ namespace s6 {
 // output pass at 16 states, which the compiler otherwise lays out at 129 VGPRs (3 waves;
 // measured 5% slower).  The raw / bias z-gated variants would spill at 128 and keep the
 // default.
-template <typename Tio, typename Tbc, int NS, int MODE, int DTM, bool MULTI>
+// VEC (p.rowvec; not with MULTI): u / delta / z / out / out_z have a contiguous time axis,
+// 16-byte aligned at every block of 8 steps, and every chunk is whole blocks; each lane then
+// moves a block of its row with one 16-byte access per tensor (Row8) instead of eight, each of
+// which would touch one cache line per lane (measured: the cfg3-shape forward with
+// checkpoints 1.00 -> 0.64 ms, the z-gated softplus forward at B32 L4096 D256 1.13 -> 0.51 ms,
+// both on [B, D, L] L-contiguous inputs).
+template <typename Tio, typename Tbc, int NS, int MODE, int DTM, bool MULTI, bool VEC>
 __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     __attribute__((amdgpu_waves_per_eu((MULTI || (MODE == 2 && DTM == kDtSoftplus && NS <= 16)) ? 4 : 1)))
     fwd_scan(FwdK p) {
@@ -45,6 +51,7 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   constexpr int GS = NS < kGroupStates<Tbc> ? NS : kGroupStates<Tbc>;  // states per scalar group
   constexpr int NG = NS / GS;
   static_assert(!MULTI || NS == 16, "state groups of 16");
+  static_assert(!(MULTI && VEC), "row vectors with one wave per channel block only");
   const int lane = threadIdx.x & (kWave - 1);
   // State group of this wave, made wave-uniform (an SGPR) so that the B / C row addresses
   // derived from it stay scalar and their loads stay on the scalar cache.
@@ -132,19 +139,52 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   float ssum = 0.f;         // sum of Delta since the last sequence start (chunk summary only)
   bool seen_start = false;  // a sequence started inside this chunk
 
-  // Register double buffer: the next block's u / delta / z are in flight, as raw bits, while
-  // the current block computes.  Loads past t1 re-read step t1 - 1.
-  uint32_t un[TB], dn[TB], zn[TB];
+  // Per-step form (!VEC): a register double buffer; the next block's u / delta / z are in
+  // flight, as raw bits, while the current block computes, and loads past t1 re-read step
+  // t1 - 1.  Outputs and checkpoints are stored as they are computed.
+  // Row-block form (VEC): a block begins by taking over its rows (loaded one block earlier),
+  // then stores the previous block's outputs and checkpoint, then issues the next block's
+  // loads, and its steps issue no vector memory operation.  The compiler waits for a load
+  // with vmcnt(0) whenever stores are in flight, so this order makes the one wait per block,
+  // at the takeover, cover only operations a block old.  (The same order in the per-step
+  // form measured 3-9% slower: the held outputs cost registers there.)
+  uint32_t un[VEC ? 1 : TB], dn[VEC ? 1 : TB], zn[VEC ? 1 : TB];
+  Row8<Tio> vu, vd, vz;  // VEC: the next block's rows
   auto fetch = [&](int tb) {
+    const uint32_t r = (uint32_t)(tb - t0);
+    if constexpr (VEC) {
+      vu.load(rs_u, vo_u, r * st_u);
+      vd.load(rs_d, vo_d, r * st_d);
+      if (HAS_Z) vz.load(rs_z, vo_z, r * st_z);
+    } else {
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
-      un[i] = Buf<Tio>::load_raw(rs_u, vo_u, r * st_u);
-      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
-      if (HAS_Z && !MULTI) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
+      for (int i = 0; i < TB; ++i) {
+        const uint32_t ri = (uint32_t)(min(tb + i, t1 - 1) - t0);
+        un[i] = Buf<Tio>::load_raw(rs_u, vo_u, ri * st_u);
+        dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, ri * st_d);
+        if (HAS_Z && !MULTI) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, ri * st_z);
+      }
     }
   };
   fetch(t0);
+  if constexpr (VEC) {
+    // The loop's first use of a block's rows would otherwise inherit this load's wait, which
+    // on later blocks would also cover the stores issued just before it.
+    vu.settle();
+    vd.settle();
+    if (HAS_Z) vz.settle();
+  }
+  // VEC: the previous block's packed outputs, stored at the top of the next block (or after
+  // the loop); h still holds the block's final state there, which is its checkpoint.
+  Row8<Tio> po, poz;
+  auto flush = [&](int tbp) {
+    if constexpr (VEC && FULL) {
+      const uint32_t r = (uint32_t)(tbp - t0);
+      po.store(rs_o, vo_o, r * st_o);
+      if (HAS_Z) poz.store(rs_oz, vo_oz, r * st_oz);
+      if (xck != nullptr && active) store_state<NS>(xck + (int64_t)(tbp / kCk) * xck_step, h, Nw);
+    }
+  };
 
   // Scalar-cache pipeline for B_t / C_t (touch / opaque, s6_common.h): one group of GS
   // states is in flight while the previous one is consumed.
@@ -153,12 +193,20 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   if (FULL) cnx.template load<GS>(Cbase);
 
   for (int tb = t0; tb < t1; tb += TB) {
-    float uc[TB], dc[TB], zc[TB];
+    float uc[VEC ? 1 : TB], dc[VEC ? 1 : TB], zc[VEC ? 1 : TB];
+    Row8<Tio> ru, rd, rz;  // VEC: this block's rows
+    if constexpr (VEC) {
+      ru = vu;
+      rd = vd;
+      if (HAS_Z) rz = vz;
+      if (tb > t0) flush(tb - TB);
+    } else {
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      uc[i] = Buf<Tio>::from_raw(un[i]);
-      dc[i] = Buf<Tio>::from_raw(dn[i]);
-      zc[i] = (HAS_Z && !MULTI) ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+      for (int i = 0; i < TB; ++i) {
+        uc[i] = Buf<Tio>::from_raw(un[i]);
+        dc[i] = Buf<Tio>::from_raw(dn[i]);
+        zc[i] = (HAS_Z && !MULTI) ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+      }
     }
     // MULTI output pass: u (and z) of the steps this wave finishes after the block,
     // i = gn + k nsg, reloaded now (they are in cache from the prefetch) so that the block's
@@ -175,13 +223,20 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         }
       }
     }
-    if (tb + TB < t1) fetch(tb + TB);
+    // VEC: unconditional (the last block re-reads itself), so that the next block's rows are
+    // always a fresh load; a skipped load would merge the old value back in, and the compiler
+    // then copies the fresh one right after its load, which waits for it.
+    if constexpr (VEC) fetch(min(tb + TB, t1 - TB));
+    else if (tb + TB < t1) fetch(tb + TB);
     // A sequence starts inside this block, or right after it (its predecessor's final
     // state is stored at the block's last step).
     const bool blk_has_start = varlen && sc.pending <= (int64_t)tb + TB;
     // Blocks that are full, hold no sequence boundary and do not end the input take the
     // fast path: no per-step bounds, reset or final-state checks.
     const bool general = blk_has_start || tb + TB > t1 || (FULL && tb + TB >= L);
+    // VEC: the block's outputs, packed after the general / fast paths join (packed inside
+    // them, the compiler keeps both paths' values apart: about 90 more VGPRs).
+    float yb[TB];
     auto block = [&](auto gen_tag) {
       constexpr bool GEN = decltype(gen_tag)::value;
 #pragma unroll
@@ -198,8 +253,8 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         }
         const uint32_t r = (uint32_t)(t - t0);
         const uint32_t rn = (uint32_t)(min(t + 1, t1 - 1) - t0);
-        const float uu = uc[i];
-        const float dt = prep_dt<DTM>(dc[i], bias);
+        const float uu = VEC ? ru.get(i) : uc[VEC ? 0 : i];
+        const float dt = prep_dt<DTM>(VEC ? rd.get(i) : dc[VEC ? 0 : i], bias);
         const float dtu = dt * uu;
         // y accumulates in 4 independent FMA chains (n mod 4): shorter dependency chains
         // and a smaller rounding error than one long chain.
@@ -229,11 +284,13 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
           float y = (ys[0] + ys[1]) + (ys[2] + ys[3]);
           if constexpr (MULTI) {
             ysh[((tb - t0) / TB) & 1][gn][i][lane] = y;  // this group's share of y
+          } else if constexpr (VEC) {
+            yb[i] = fmaf(uu, Dv, y);
           } else {
             y = fmaf(uu, Dv, y);
             Buf<Tio>::store(rs_o, vo_o, r * st_o, y);
             if (HAS_Z) {
-              const float zz = zc[i];
+              const float zz = zc[VEC ? 0 : i];
               Buf<Tio>::store(rs_oz, vo_oz, r * st_oz, y * zz * sigmoidf_(zz));
             }
           }
@@ -250,7 +307,7 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
               if (active && row_ok) store_state<NS>(p.last_state + (row * p.D + d) * p.N + s0, h, Nw);
             }
           }
-          if ((i == TB - 1 || (GEN && t == L - 1)) && xck != nullptr) {
+          if (!VEC && (i == TB - 1 || (GEN && t == L - 1)) && xck != nullptr) {
             if (active) store_state<NS>(xck + (int64_t)(t / kCk) * xck_step, h, Nw);
           }
         }
@@ -282,7 +339,19 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
       }
     };
     if (general) block(std::true_type{}); else block(std::false_type{});
+    if constexpr (VEC && FULL) {
+      po.pack(yb);
+      if constexpr (HAS_Z) {
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+          const float zz = rz.get(i);
+          yb[i] = yb[i] * zz * sigmoidf_(zz);
+        }
+        poz.pack(yb);
+      }
+    }
   }
+  if constexpr (VEC) flush(t1 - TB);
   if (!FULL && active) {
     store_state<NS>(p.ws_h + (ch * p.K + c) * p.N + s0, h, Nw);
     if (gn == 0) {
@@ -293,26 +362,35 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
 }
 
 // ---------------------------------------------------------------------------------------
-// Host-side launch helpers
+// Host-side launch helpers.  The translation unit is compiled twice per input dtype: with
+// S6_FWD_VEC=1 it instantiates the row-vector kernels (VEC) and defines
+// launch_fwd_rowvec_io, otherwise the per-step kernels and launch_fwd_io, which routes
+// row-vector problems to the other unit.
 // ---------------------------------------------------------------------------------------
+
+#ifndef S6_FWD_VEC
+#define S6_FWD_VEC 0
+#endif
+constexpr bool kVec = S6_FWD_VEC != 0;
 
 template <typename Tio, typename Tbc, int NS, int DTM, bool MULTI>
 static hipError_t launch_scan_pair(const FwdK& k, hipStream_t st, void* const* ev) {
+  constexpr bool V = kVec && !MULTI;
   hipError_t e = hipSuccess;
   const dim3 grid = xcd_grid(k.Bsz * k.nDblk, k.K);
   const dim3 block(MULTI ? (unsigned)(k.nsg * kWave) : (unsigned)kWave);
   if (k.K > 1) {
     // Summaries of chunks 0..K-2: the last chunk's summary is never used.
     const dim3 gsum = xcd_grid(k.Bsz * k.nDblk, k.K - 1);
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 0, DTM, MULTI>), gsum, block, 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 0, DTM, MULTI, V>), gsum, block, 0, st, k);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_fwd_carry(k, st)) != hipSuccess) return e;
   }
   if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
   if (k.has_z)
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 2, DTM, MULTI>), grid, block, 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 2, DTM, MULTI, V>), grid, block, 0, st, k);
   else
-    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 1, DTM, MULTI>), grid, block, 0, st, k);
+    hipLaunchKernelGGL((fwd_scan<Tio, Tbc, NS, 1, DTM, MULTI, V>), grid, block, 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return record_event(ev, 1, st);
 }
@@ -331,17 +409,29 @@ static hipError_t launch_bc(const FwdK& k, hipStream_t st, void* const* ev) {
   if (k.N <= 8) return launch_dt<Tio, Tbc, 8, false>(k, st, ev);
   if (k.N <= 16) return launch_dt<Tio, Tbc, 16, false>(k, st, ev);
   if (k.N <= 32) return launch_dt<Tio, Tbc, 32, false>(k, st, ev);
-  return launch_dt<Tio, Tbc, 16, true>(k, st, ev);  // k.nsg groups of 16 states
+  if constexpr (kVec) return hipErrorInvalidValue;  // the host routes dstate > 32 elsewhere
+  else return launch_dt<Tio, Tbc, 16, true>(k, st, ev);  // k.nsg groups of 16 states
 }
 
+#if S6_FWD_VEC
+template <typename Tio>
+hipError_t launch_fwd_rowvec_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (bc_dtype == S6_F32) return launch_bc<Tio, float>(k, st, ev);
+  return launch_bc<Tio, Tio>(k, st, ev);
+}
+
+template hipError_t launch_fwd_rowvec_io<S6_TIO>(const FwdK&, int, hipStream_t, void* const*);
+#else
 template <typename Tio>
 hipError_t launch_fwd_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
   if (k.lanes) return launch_fwd_lanes_io<Tio>(k, bc_dtype, st, ev);
+  if (k.rowvec) return launch_fwd_rowvec_io<Tio>(k, bc_dtype, st, ev);
   // B / C are either in the input dtype or fp32 (the interface enforces it).
   if (bc_dtype == S6_F32) return launch_bc<Tio, float>(k, st, ev);
   return launch_bc<Tio, Tio>(k, st, ev);
 }
 
 template hipError_t launch_fwd_io<S6_TIO>(const FwdK&, int, hipStream_t, void* const*);
+#endif
 
 }  // namespace s6

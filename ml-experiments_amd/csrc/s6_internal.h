@@ -253,6 +253,8 @@ template <typename Tio>
 hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
 template <typename Tio>
 hipError_t launch_fwd_lanes_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
+template <typename Tio>
+hipError_t launch_fwd_rowvec_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
 
 // s6_misc.hip: carries, reductions, fills, B/C relayout.
 hipError_t launch_fwd_carry(const FwdK& k, hipStream_t st);

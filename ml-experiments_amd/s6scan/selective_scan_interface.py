@@ -180,6 +180,49 @@ def _ckpt_strides(x_ckpt):
     return (0,) * 4 if x_ckpt is None else tuple(x_ckpt.stride()[:3]) + (1,)
 
 
+def _fwd_args(prob, u, delta, A, B4, C4, D, z, delta_bias, cu_seqlens, out, out_z, x_ckpt,
+              last_state):
+    args = _lib.S6FwdArgs()
+    args.p = prob
+    args.u, args.u_stride = _ptr(u), _strides(u, 3)
+    args.delta, args.delta_stride = _ptr(delta), _strides(delta, 3)
+    args.A, args.A_stride = _ptr(A), _strides(A, 2)
+    args.B, args.B_stride = _ptr(B4), _strides(B4, 4)
+    args.C, args.C_stride = _ptr(C4), _strides(C4, 4)
+    args.D, args.D_stride = _ptr(D), (D.stride(0) if D is not None else 0)
+    args.z, args.z_stride = _ptr(z), _strides(z, 3)
+    args.delta_bias = _ptr(delta_bias)
+    args.delta_bias_stride = delta_bias.stride(0) if delta_bias is not None else 0
+    args.cu_seqlens = _ptr(cu_seqlens)
+    args.out, args.out_stride = _ptr(out), _strides(out, 3)
+    args.out_z, args.out_z_stride = _ptr(out_z), _strides(out_z, 3)
+    args.x_ckpt, args.x_ckpt_stride = _ptr(x_ckpt), _ckpt_strides(x_ckpt)
+    args.last_state = _ptr(last_state)
+    return args
+
+
+def forward_row_blocks(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                       cu_seqlens=None):
+    """True if selective_scan_forward on these tensors (outputs laid out like u, as it
+    allocates them) runs the chunked kernels with whole 8-step row blocks per lane
+    (``s6_fwd_row_blocks``); False for per-step accesses or the single-pass kernel.  Host
+    only: no kernel runs and nothing is allocated on the device."""
+    dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
+    prob = _problem(u, B, z, D, delta_bias, delta_softplus, dims)
+    args = _fwd_args(prob, u, delta, A, _as4(B), _as4(C), D, z, delta_bias, cu_seqlens, u,
+                     u if z is not None else None, None, None)
+    # The outputs stand in as u's pointer with the strides empty_like(u) gives them; only
+    # their layout and alignment enter the choice, which needs u aligned as well.
+    like = _strides(torch.empty_like(u, device="meta"), 3)
+    args.out_stride = like
+    if z is not None:
+        args.out_z_stride = like
+    rc = _lib.LIB.s6_fwd_row_blocks(ctypes.byref(args))
+    if rc < 0:
+        _lib.check(rc, "s6_fwd_row_blocks")
+    return rc == 1
+
+
 def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
                            delta_softplus=False, cu_seqlens=None, want_ckpt=True,
                            want_last_state=False, kernel_events=None, x_ckpt_out=None,
@@ -210,22 +253,8 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
         nls = nseq if nseq > 0 else batch
         last_state = (torch.empty(nls, dim, dstate, dtype=torch.float32, device=u.device)
                       if want_last_state else None)
-        args = _lib.S6FwdArgs()
-        args.p = prob
-        args.u, args.u_stride = _ptr(u), _strides(u, 3)
-        args.delta, args.delta_stride = _ptr(delta), _strides(delta, 3)
-        args.A, args.A_stride = _ptr(A), _strides(A, 2)
-        args.B, args.B_stride = _ptr(B4), _strides(B4, 4)
-        args.C, args.C_stride = _ptr(C4), _strides(C4, 4)
-        args.D, args.D_stride = _ptr(D), (D.stride(0) if D is not None else 0)
-        args.z, args.z_stride = _ptr(z), _strides(z, 3)
-        args.delta_bias = _ptr(delta_bias)
-        args.delta_bias_stride = delta_bias.stride(0) if delta_bias is not None else 0
-        args.cu_seqlens = _ptr(cu_seqlens)
-        args.out, args.out_stride = _ptr(out), _strides(out, 3)
-        args.out_z, args.out_z_stride = _ptr(out_z), _strides(out_z, 3)
-        args.x_ckpt, args.x_ckpt_stride = _ptr(x_ckpt), _ckpt_strides(x_ckpt)
-        args.last_state = _ptr(last_state)
+        args = _fwd_args(prob, u, delta, A, B4, C4, D, z, delta_bias, cu_seqlens, out, out_z,
+                         x_ckpt, last_state)
         args.kernel_events = _events(kernel_events)
         stream = torch.cuda.current_stream(u.device).cuda_stream
         if no_alloc:

@@ -298,6 +298,42 @@ def test_forward_kernel_choice(monkeypatch):
     assert q(batch=0) == _lib.E_INVALID
 
 
+def test_forward_row_block_choice(monkeypatch):
+    """s6_fwd_row_blocks says whether the chunked forward moves u / delta / z / out / out_z in
+    whole 8-step row blocks: only for a contiguous time axis with 16-byte aligned rows and
+    blocks, seqlen a multiple of 8, dstate <= 32 and not the single-pass kernel; the
+    environment override S6_FWD_ROWVEC=0 turns it off.  Host-only (fake pointers)."""
+    monkeypatch.delenv("S6_FWD_ROWVEC", raising=False)
+    monkeypatch.setenv("S6_FWD_PATH", "chunked")
+    q = lambda a: _lib.LIB.s6_fwd_row_blocks(ctypes.byref(a))
+    assert q(fwd_args(seqlen=1024)) == 1                       # [B, D, L] L-contiguous
+    assert q(fwd_args(seqlen=1000)) == 1                       # 1000 = 125 blocks of 8
+    assert q(fwd_args(seqlen=1004)) == 0                       # a partial last block
+    assert q(fwd_args(seqlen=1024, dstate=32)) == 1
+    assert q(fwd_args(seqlen=1024, dstate=48)) == 0            # one wave per 16 states
+    a = fwd_args(seqlen=1024)
+    a.u_stride = (a.p.dim * 1024, 1, a.p.dim)                  # channel-last view
+    assert q(a) == 0
+    a = fwd_args(seqlen=1024)
+    a.out = 0x10000 + 8                                        # out rows 8-byte aligned only
+    assert q(a) == 0
+    a = fwd_args(seqlen=1024, io_dtype=_lib.F32, bc_dtype=_lib.F32)
+    a.delta_stride = (a.p.dim * 1026, 1026, 1)                 # rows 4104 B apart: not 16-aligned
+    assert q(a) == 0
+    a = fwd_args(seqlen=1024, has_z=1)
+    assert q(a) == _lib.E_INVALID                              # z / out_z missing
+    a.z = a.out_z = 0x20000
+    a.z_stride = a.out_z_stride = a.u_stride
+    assert q(a) == 1
+    a.out_z_stride = (a.p.dim * 1024, 1, a.p.dim)
+    assert q(a) == 0
+    monkeypatch.setenv("S6_FWD_ROWVEC", "0")
+    assert q(fwd_args(seqlen=1024)) == 0
+    monkeypatch.delenv("S6_FWD_ROWVEC")
+    monkeypatch.setenv("S6_FWD_PATH", "lanes")
+    assert q(fwd_args(batch=32, dim=256, seqlen=4096)) == 0    # the single-pass kernel
+
+
 def _ssd_problem(P=64, N=32, Q=64, z=0, L=300, H=4, G=2, batch=2):
     return _lib.S6SsdProblem(batch, L, H, P, G, N, Q, _lib.BF16, 1, 0, z, 1, 1, 0, 0, 0.0,
                              float("inf"))

@@ -105,14 +105,23 @@ FWD_CASES = [
     (2, 129, 128, 16, torch.bfloat16, 1, False, False, "contiguous"),
     (2, 129, 128, 16, torch.bfloat16, 1, False, False, "bc_lcontig"),
     (1, 2000, 64, 16, torch.float32, 1, False, False, "view"),
+    # L-contiguous with seqlen a multiple of 8: whole 8-step row blocks per lane
+    (2, 264, 128, 16, torch.float32, 1, True, True, "contiguous"),
+    (2, 264, 96, 16, torch.float16, 1, True, False, "contiguous"),
+    (1, 520, 64, 8, torch.bfloat16, 1, False, True, "contiguous"),
+    (2, 136, 128, 32, torch.bfloat16, 1, True, False, "contiguous"),
 ]
 
 
 @pytest.mark.parametrize("case", FWD_CASES, ids=lambda c: "-".join(map(str, c)).replace("torch.", ""))
 def test_forward_matches_restatement(case):
+    """fp32 cases are held to the fp32 bar against the float64 evaluation of the restatement:
+    the fp32 evaluation is itself up to ~4e-6 off the exact value on these inputs (measured
+    on the z-gated softplus case at seqlen 264), more than the 1e-6 absolute bar, and its
+    rounding changes with the host's thread count."""
     B, L, D, N, dtype, G, z, bias, layout = case
     inp = gen(B, L, D, N, dtype, seed=L + D + N, G=G, z=z, bias=bias)
-    out_ref, ls_ref = ref_fwd(inp)
+    out_ref, ls_ref = ref_fwd64(inp) if dtype == torch.float32 else ref_fwd(inp)
     args, kw = call(inp, layout, DEV)
     out, ls = s6scan.selective_scan_fn(*args, **kw)
     assert out.dtype == dtype and out.shape == (B, D, L)
