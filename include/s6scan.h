@@ -171,6 +171,11 @@ int s6_fwd_single_pass(const S6Problem* p);
  * counterpart in the reference: it names the kernel variant a caller is timing. */
 int s6_fwd_row_blocks(const S6FwdArgs* a);
 
+/* Host-only: the same for s6_bwd (u, delta, dout, du, ddelta and, with z, z, out, dz and
+ * out_z when given; dstate <= 16; override S6_BWD_ROWVEC=0).  Checks the problem only, not
+ * the other arguments.  No counterpart in the reference. */
+int s6_bwd_row_blocks(const S6BwdArgs* a);
+
 /* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */
 int64_t s6_num_checkpoints(const S6Problem* p);
 

@@ -23,8 +23,11 @@ UNITS = [("s6_abi.cpp", "s6_abi", []), ("s6_misc.hip", "s6_misc", []),
          ("s6_ssd.hip", "s6_ssd", []), ("s6_ssd_bwd.hip", "s6_ssd_bwd", [])]
 UNITS += [(f"s6_{d}.hip", f"s6_{d}_{t}", [f"-DS6_TIO={ty}"])
           for d in ("fwd", "bwd", "fwd_lanes") for t, ty in _TIO.items()]
-# The chunked forward's row-vector kernels (S6_FWD_VEC=1) are a second unit per dtype.
+# The chunked forward's and the backward's row-block kernels (S6_FWD_VEC=1, S6_BWD_VEC=1)
+# are a second unit per dtype each.
 UNITS += [("s6_fwd.hip", f"s6_fwd_vec_{t}", [f"-DS6_TIO={ty}", "-DS6_FWD_VEC=1"])
+          for t, ty in _TIO.items()]
+UNITS += [("s6_bwd.hip", f"s6_bwd_vec_{t}", [f"-DS6_TIO={ty}", "-DS6_BWD_VEC=1"])
           for t, ty in _TIO.items()]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -302,6 +302,25 @@ bool choose_rowvec(const S6FwdArgs& a, const Plan& pl) {
   return ok;
 }
 
+// The backward's row blocks (one wave per 64-channel block, dstate <= 16): every per-channel
+// tensor it reads or writes passes rows_vec_ok.  S6_BWD_ROWVEC=0 keeps per-step accesses.
+bool choose_rowvec_bwd(const S6BwdArgs& a) {
+  const S6Problem& p = a.p;
+  if (p.dstate > s6::kBwdGroup || p.seqlen % s6::kCk != 0) return false;
+  const char* env = getenv("S6_BWD_ROWVEC");
+  if (env != nullptr && strcmp(env, "0") == 0) return false;
+  const int es = esize(p.io_dtype);
+  bool ok = rows_vec_ok(a.u, a.u_stride, es, p) && rows_vec_ok(a.delta, a.delta_stride, es, p) &&
+            rows_vec_ok(a.dout, a.dout_stride, es, p) && rows_vec_ok(a.du, a.du_stride, es, p) &&
+            rows_vec_ok(a.ddelta, a.ddelta_stride, es, p);
+  if (p.has_z) {
+    ok = ok && rows_vec_ok(a.z, a.z_stride, es, p) && rows_vec_ok(a.out, a.out_stride, es, p) &&
+         rows_vec_ok(a.dz, a.dz_stride, es, p);
+    if (a.out_z != nullptr) ok = ok && rows_vec_ok(a.out_z, a.out_z_stride, es, p);
+  }
+  return ok;
+}
+
 s6::FwdK fill_fwd(const S6FwdArgs& a, const Plan& pl) {
   s6::FwdK k{};
   const S6Problem& p = a.p;
@@ -1080,6 +1099,13 @@ size_t s6_bwd_workspace_bytes(const S6Problem* p) {
 
 int s6_validate_fwd(const S6FwdArgs* a) { return validate_fwd(a, true); }
 
+int s6_bwd_row_blocks(const S6BwdArgs* a) {
+  if (a == nullptr) return fail(S6_E_INVALID, "args must not be NULL");
+  int r = s6_validate_problem(&a->p);
+  if (r != S6_OK) return r;
+  return choose_rowvec_bwd(*a) ? 1 : 0;
+}
+
 int s6_fwd_row_blocks(const S6FwdArgs* a) {
   int r = validate_fwd(a, false);
   if (r != S6_OK) return r;
@@ -1284,6 +1310,7 @@ int s6_bwd(const S6BwdArgs* a, void* stream) {
     k.K = pl.K; k.Lc = pl.Lc;
     k.nDblk = pl.nDblk; k.nJ = pl.nJ; k.nsg = pl.nsg; k.NPr = pl.NPr;
     k.has_D = p.has_D; k.has_z = p.has_z; k.has_bias = p.has_delta_bias; k.softplus = p.delta_softplus;
+    k.rowvec = choose_rowvec_bwd(*a) ? 1 : 0;
     e = s6::launch_bwd(k, p.io_dtype, p.bc_dtype, st, a->kernel_events);
   }
   if (e != hipSuccess) return fail(S6_E_HIP, "s6_bwd: %s", hipGetErrorString(e));

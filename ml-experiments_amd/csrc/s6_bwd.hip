@@ -27,7 +27,14 @@
 
 namespace s6 {
 
-template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+// VEC (p.rowvec; bwd_scan: not with MULTI): the per-channel tensors (u, delta, dout, z, out
+// and du, ddelta, dz, out_z) have a contiguous time axis, 16-byte aligned at every block of 8
+// steps, and every chunk is whole blocks.  Each lane then moves a block of its row with one
+// 16-byte access per tensor (Row8, s6_common.h) instead of eight, each of which would touch one
+// cache line per lane.  The next block's load is issued unconditionally (the first block
+// re-reads itself): a skipped load would merge the old value back in, and the compiler then
+// copies the fresh value right after its load, which waits for it.
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool VEC>
 __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   constexpr int TB = kCk;
   constexpr int ES = Elem<Tio>::kSize;
@@ -77,18 +84,31 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
       (const char*)p.Cm + (b * p.sC[0] + g * p.sC[1] + (int64_t)t0 * p.sC[3] + s0) * EB;
   const uint32_t Cst = (uint32_t)(p.sC[3] * EB);
 
-  uint32_t on[TB], dn[TB], zn[TB];  // raw bits of the next block's inputs, in flight
+  uint32_t on[VEC ? 1 : TB], dn[VEC ? 1 : TB], zn[VEC ? 1 : TB];  // next block, raw bits
+  Row8<Tio> vo, vd, vz;                                              // VEC: next block's rows
   auto fetch = [&](int tb) {
+    if constexpr (VEC) {
+      const uint32_t r = (uint32_t)(tb - t0);
+      vo.load(rs_o, vo_o, r * st_o);
+      vd.load(rs_d, vo_d, r * st_d);
+      if (HAS_Z) vz.load(rs_z, vo_z, r * st_z);
+    } else {
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
-      on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
-      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
-      if (HAS_Z) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
+      for (int i = 0; i < TB; ++i) {
+        const uint32_t r = (uint32_t)(min(tb + i, t1 - 1) - t0);
+        on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
+        dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
+        if (HAS_Z) zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
+      }
     }
   };
   const int tlast = t0 + ((t1 - 1 - t0) / TB) * TB;  // first step of the last block
   fetch(tlast);
+  if constexpr (VEC) {
+    vo.settle();
+    vd.settle();
+    if (HAS_Z) vz.settle();
+  }
   BCGroup<Tbc> cnx;
   cnx.template load<GS>(Cbase + (uint32_t)(t1 - 1 - t0) * Cst);
   float ssum = 0.f;
@@ -97,23 +117,34 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
   if (varlen) rc = seq_cursor_rev_at(p.cu, p.nseq, t1);
 
   for (int tb = tlast; tb >= t0; tb -= TB) {
-    float oc[TB], dc[TB], zc[TB];
+    float oc[VEC ? 1 : TB], dc[VEC ? 1 : TB], zc[VEC ? 1 : TB];
+    Row8<Tio> ro, rd, rz;  // VEC: this block's rows, unpacked where used
+    if constexpr (VEC) {
+      ro = vo;
+      rd = vd;
+      if (HAS_Z) rz = vz;
+      fetch(max(tb - TB, t0));
+    } else {
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-      oc[i] = Buf<Tio>::from_raw(on[i]);
-      dc[i] = Buf<Tio>::from_raw(dn[i]);
-      zc[i] = HAS_Z ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+      for (int i = 0; i < TB; ++i) {
+        oc[i] = Buf<Tio>::from_raw(on[i]);
+        dc[i] = Buf<Tio>::from_raw(dn[i]);
+        zc[i] = HAS_Z ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+      }
+      if (tb > t0) fetch(tb - TB);
     }
-    if (tb > t0) fetch(tb - TB);
     const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, tb) : 0u;
     seen_start = seen_start || smask != 0u;
 #pragma unroll
     for (int i = TB - 1; i >= 0; --i) {
       const int t = tb + i;
       if (t < t1) {
-        float dy = oc[i];
-        if (HAS_Z) dy *= zc[i] * sigmoidf_(zc[i]);
-        const float dt = prep_dt<DTM>(dc[i], bias);
+        float dy = VEC ? ro.get(i) : oc[VEC ? 0 : i];
+        if (HAS_Z) {
+          const float zz = VEC ? rz.get(i) : zc[VEC ? 0 : i];
+          dy *= zz * sigmoidf_(zz);
+        }
+        const float dt = prep_dt<DTM>(VEC ? rd.get(i) : dc[VEC ? 0 : i], bias);
         const uint32_t r = (uint32_t)(t - t0);
         const uint32_t rn = (uint32_t)(max(t - 1, t0) - t0);
 #pragma unroll
@@ -156,9 +187,10 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
 // channels and chunk (p.nsg waves).  After each segment the waves exchange their per-step
 // sums over states (sum lambda B, sum q A) through LDS, and wave gn finishes the steps
 // gn, gn + nsg, ...: groups summed in order 0..nsg-1, du, dDelta and the ddelta_bias share.
-template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI>
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI, bool VEC>
 __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_scan(BwdK p) {
+  static_assert(!(MULTI && VEC), "row blocks with one wave per channel block only");
   constexpr int SEG = kCk;  // steps per segment = checkpoint interval
   constexpr int HS = 8;     // states per half
   constexpr int NH = NS / HS;
@@ -268,19 +300,32 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   // row is loaded unconditionally from an in-bounds row (row 0 for the first segment, the
   // group's last real state for padded ones) and masked at use, so no load waits or branches
   // in the prefetch.
-  uint32_t un[SEG], dn[SEG], on[SEG], zn[SEG], yn[SEG];
+  constexpr int RW = VEC ? 1 : SEG;
+  uint32_t un[RW], dn[RW], on[RW], zn[RW], yn[RW];
+  Row8<Tio> vu, vd, vo, vz, vy;  // VEC: the next segment's rows
   float hn[NS];
   auto fetch = [&](int ts) {
     const int te = min(ts + SEG, t1);
-#pragma unroll
-    for (int i = 0; i < SEG; ++i) {
-      const uint32_t r = (uint32_t)(min(ts + i, te - 1) - t0);
-      un[i] = Buf<Tio>::load_raw(rs_u, vo_u, r * st_u);
-      dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
-      on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
+    if constexpr (VEC) {
+      const uint32_t r = (uint32_t)(ts - t0);
+      vu.load(rs_u, vo_u, r * st_u);
+      vd.load(rs_d, vo_d, r * st_d);
+      vo.load(rs_o, vo_o, r * st_o);
       if (HAS_Z) {
-        zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
-        yn[i] = Buf<Tio>::load_raw(rs_y, vo_y, r * st_y);
+        vz.load(rs_z, vo_z, r * st_z);
+        vy.load(rs_y, vo_y, r * st_y);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < SEG; ++i) {
+        const uint32_t r = (uint32_t)(min(ts + i, te - 1) - t0);
+        un[i] = Buf<Tio>::load_raw(rs_u, vo_u, r * st_u);
+        dn[i] = Buf<Tio>::load_raw(rs_d, vo_d, r * st_d);
+        on[i] = Buf<Tio>::load_raw(rs_o, vo_o, r * st_o);
+        if (HAS_Z) {
+          zn[i] = Buf<Tio>::load_raw(rs_z, vo_z, r * st_z);
+          yn[i] = Buf<Tio>::load_raw(rs_y, vo_y, r * st_y);
+        }
       }
     }
     // the state after step ts - 1 (used only for ts > 0: zero at the start of the input)
@@ -290,6 +335,15 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
   };
   const int nseg = (t1 - t0 + SEG - 1) / SEG;
   fetch(t0 + (nseg - 1) * SEG);
+  if constexpr (VEC) {
+    vu.settle();
+    vd.settle();
+    vo.settle();
+    if (HAS_Z) {
+      vz.settle();
+      vy.settle();
+    }
+  }
   SeqCursorRev rc{0, -1};  // segments are visited from the last one down
   if (varlen) rc = seq_cursor_rev_at(p.cu, p.nseq, t1);
 
@@ -307,28 +361,55 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     const int ts = t0 + s * SEG;
     const int te = min(ts + SEG, t1);
     float uu[SEG], dt[SEG], dy[SEG], pre[SEG], hst[NS];
+    Row8<Tio> cu, cd, co, cz, cy;  // VEC: this segment's rows
+    if constexpr (VEC) {
+      cu = vu;
+      cd = vd;
+      co = vo;
+      if (HAS_Z) {
+        cz = vz;
+        cy = vy;
+      }
+    }
+    float dzv[SEG], ozv[SEG];  // VEC: the gate's gradient and out_z, stored as row blocks
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
-      const float dl = Buf<Tio>::from_raw(dn[i]), oo = Buf<Tio>::from_raw(on[i]);
-      uu[i] = Buf<Tio>::from_raw(un[i]);
+      const float dl = VEC ? cd.get(i) : Buf<Tio>::from_raw(dn[VEC ? 0 : i]);
+      const float oo = VEC ? co.get(i) : Buf<Tio>::from_raw(on[VEC ? 0 : i]);
+      uu[i] = VEC ? cu.get(i) : Buf<Tio>::from_raw(un[VEC ? 0 : i]);
       pre[i] = dl + bias;
       dt[i] = prep_dt<DTM>(dl, bias);
       dy[i] = oo;
       if (HAS_Z) {
         // out_z = out * silu(z):  dy = dout silu(z),  dz = dout out sig (1 + z (1 - sig))
-        const float zz = Buf<Tio>::from_raw(zn[i]), yy = Buf<Tio>::from_raw(yn[i]);
+        const float zz = VEC ? cz.get(i) : Buf<Tio>::from_raw(zn[VEC ? 0 : i]);
+        const float yy = VEC ? cy.get(i) : Buf<Tio>::from_raw(yn[VEC ? 0 : i]);
         const float sg = sigmoidf_(zz);
         dy[i] = oo * (zz * sg);
-        if (ts + i < te && gn == 0) {
-          Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz,
-                          oo * yy * sg * (1.f + zz * (1.f - sg)));
-          if (want_oz) Buf<Tio>::store(rs_oz, vo_oz, (uint32_t)(ts + i - t0) * st_oz, yy * (zz * sg));
+        const float dzi = oo * yy * sg * (1.f + zz * (1.f - sg));
+        const float ozi = yy * (zz * sg);
+        if constexpr (VEC) {
+          dzv[i] = dzi;
+          ozv[i] = ozi;
+        } else if (ts + i < te && gn == 0) {
+          Buf<Tio>::store(rs_dz, vo_dz, (uint32_t)(ts + i - t0) * st_dz, dzi);
+          if (want_oz) Buf<Tio>::store(rs_oz, vo_oz, (uint32_t)(ts + i - t0) * st_oz, ozi);
         }
+      }
+    }
+    if constexpr (VEC && HAS_Z) {
+      Row8<Tio> pz;
+      pz.pack(dzv);
+      pz.store(rs_dz, vo_dz, (uint32_t)(ts - t0) * st_dz);
+      if (want_oz) {
+        pz.pack(ozv);
+        pz.store(rs_oz, vo_oz, (uint32_t)(ts - t0) * st_oz);
       }
     }
 #pragma unroll
     for (int n = 0; n < NS; ++n) hst[n] = (ts > 0 && n < N) ? hn[n] : 0.f;
-    if (s > 0) fetch(ts - SEG);
+    if constexpr (VEC) fetch(max(ts - SEG, t0));
+    else if (s > 0) fetch(ts - SEG);
     const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, ts) : 0u;
     float s1[SEG], s2[SEG];
 #pragma unroll
@@ -475,7 +556,10 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
       }
       __syncthreads();
     }
-    // Per-step outputs of the segment.
+    // Per-step outputs of the segment.  VEC: packed two steps at a time and stored as row
+    // blocks after the loop (the segment is whole).
+    Row8<Tio> pdu, pdd;
+    float due = 0.f, dde = 0.f;
 #pragma unroll
     for (int i = 0; i < SEG; ++i) {
       if (MULTI) {
@@ -489,16 +573,30 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         s1[i] = S1;
         s2[i] = S2;
       }
-      if (ts + i < te) {
+      if (VEC || ts + i < te) {
         const uint32_t r = (uint32_t)(ts + i - t0);
         const float duv = fmaf(dt[i], s1[i], Dv * dy[i]);
         float ddv = fmaf(uu[i], s1[i], s2[i] * 0.69314718055994531f);  // Ap = A log2(e)
         if (DTM == kDtSoftplus) ddv *= softplus20_grad(pre[i]);
-        Buf<Tio>::store(rs_du, vo_du, r * st_du, duv);
-        Buf<Tio>::store(rs_dd, vo_dd, r * st_dd, ddv);
+        if constexpr (VEC) {
+          if (i & 1) {
+            pdu.set2(i >> 1, due, duv);
+            pdd.set2(i >> 1, dde, ddv);
+          } else {
+            due = duv;
+            dde = ddv;
+          }
+        } else {
+          Buf<Tio>::store(rs_du, vo_du, r * st_du, duv);
+          Buf<Tio>::store(rs_dd, vo_dd, r * st_dd, ddv);
+        }
         if (!MULTI) dDacc = fmaf(dy[i], uu[i], dDacc);
         dbacc += ddv;
       }
+    }
+    if constexpr (VEC) {
+      pdu.store(rs_du, vo_du, (uint32_t)(ts - t0) * st_du);
+      pdd.store(rs_dd, vo_dd, (uint32_t)(ts - t0) * st_dd);
     }
   }
   // MULTI: the ddelta_bias shares of the groups' steps, summed by group 0 in group order.
@@ -525,22 +623,31 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
 
 // ---------------------------------------------------------------------------------------
 
+// The translation unit is compiled twice per input dtype: with S6_BWD_VEC=1 it instantiates
+// the row-block kernels (VEC) and defines launch_bwd_rowvec_io, otherwise the per-step
+// kernels and launch_bwd_io, which routes row-block problems to the other unit.
+#ifndef S6_BWD_VEC
+#define S6_BWD_VEC 0
+#endif
+constexpr bool kVec = S6_BWD_VEC != 0;
+
 template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool MULTI>
 static hipError_t launch_bwd_t(const BwdK& k, hipStream_t st, void* const* ev) {
+  constexpr bool V = kVec && !MULTI;
   hipError_t e;
   const int64_t nx = k.Bsz * k.nDblk;
   if (k.K > 1) {
-    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, NS, DTM, HAS_Z>), xcd_grid(nx, (k.K - 1) * k.nsg),
+    hipLaunchKernelGGL((bwd_summary<Tio, Tbc, NS, DTM, HAS_Z, V>), xcd_grid(nx, (k.K - 1) * k.nsg),
                        dim3(kWave), 0, st, k);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = launch_bwd_carry(k, st)) != hipSuccess) return e;
   }
   if ((e = record_event(ev, 0, st)) != hipSuccess) return e;
   if (MULTI) {  // one workgroup of nsg waves per chunk, 16 KB of LDS per wave
-    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K),
+    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI, V>), xcd_grid(nx, k.K),
                        dim3((unsigned)(k.nsg * kWave)), (unsigned)(k.nsg * kCk * 2 * kWave * 16), st, k);
   } else {
-    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI>), xcd_grid(nx, k.K),
+    hipLaunchKernelGGL((bwd_scan<Tio, Tbc, NS, DTM, HAS_Z, MULTI, V>), xcd_grid(nx, k.K),
                        dim3(kWave), 0, st, k);
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -567,15 +674,27 @@ template <typename Tio, typename Tbc>
 static hipError_t launch_bwd_bc(const BwdK& k, hipStream_t st, void* const* ev) {
   if (k.N <= 8) return launch_bwd_dt<Tio, Tbc, 8, false>(k, st, ev);
   if (k.N <= 16) return launch_bwd_dt<Tio, Tbc, 16, false>(k, st, ev);
-  return launch_bwd_dt<Tio, Tbc, 16, true>(k, st, ev);
+  if constexpr (kVec) return hipErrorInvalidValue;  // the host routes dstate > 16 elsewhere
+  else return launch_bwd_dt<Tio, Tbc, 16, true>(k, st, ev);
 }
 
+#if S6_BWD_VEC
+template <typename Tio>
+hipError_t launch_bwd_rowvec_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (bc_dtype == S6_F32) return launch_bwd_bc<Tio, float>(k, st, ev);
+  return launch_bwd_bc<Tio, Tio>(k, st, ev);
+}
+
+template hipError_t launch_bwd_rowvec_io<S6_TIO>(const BwdK&, int, hipStream_t, void* const*);
+#else
 template <typename Tio>
 hipError_t launch_bwd_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
+  if (k.rowvec) return launch_bwd_rowvec_io<Tio>(k, bc_dtype, st, ev);
   if (bc_dtype == S6_F32) return launch_bwd_bc<Tio, float>(k, st, ev);
   return launch_bwd_bc<Tio, Tio>(k, st, ev);
 }
 
 template hipError_t launch_bwd_io<S6_TIO>(const BwdK&, int, hipStream_t, void* const*);
+#endif
 
 }  // namespace s6

@@ -123,6 +123,8 @@ struct BwdK {
   int64_t nsg;     // state groups of 16 (1 when dstate <= 16)
   int64_t NPr;     // row width of the dB / dC partials (16 * nsg, zero-padded)
   int32_t has_D, has_z, has_bias, softplus;
+  int32_t rowvec;  // 1: whole 8-step row blocks per lane (Row8; last, so the other fields keep
+                   // the offsets the kernels were measured with)
 };
 
 // States per group of the backward kernels (a dstate above it is split into groups).
@@ -255,6 +257,8 @@ template <typename Tio>
 hipError_t launch_fwd_lanes_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
 template <typename Tio>
 hipError_t launch_fwd_rowvec_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
+template <typename Tio>
+hipError_t launch_bwd_rowvec_io(const BwdK& k, int bc_dtype, hipStream_t st, void* const* ev);
 
 // s6_misc.hip: carries, reductions, fills, B/C relayout.
 hipError_t launch_fwd_carry(const FwdK& k, hipStream_t st);

@@ -210,6 +210,7 @@ EXPORTS = {
     "s6_validate_cu_seqlens": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]),
     "s6_fwd_single_pass": (ctypes.c_int, [ctypes.POINTER(S6Problem)]),
     "s6_fwd_row_blocks": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs)]),
+    "s6_bwd_row_blocks": (ctypes.c_int, [ctypes.POINTER(S6BwdArgs)]),
     "s6_num_checkpoints": (ctypes.c_int64, [ctypes.POINTER(S6Problem)]),
     "s6_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),
     "s6_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),

@@ -269,6 +269,34 @@ def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,
     return out, out_z, x_ckpt, last_state
 
 
+def backward_row_blocks(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, out=None,
+                        cu_seqlens=None, recompute_out_z=False):
+    """True if selective_scan_backward on these tensors (its outputs laid out as it allocates
+    them) runs the row-block kernels (``s6_bwd_row_blocks``).  Host only."""
+    dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
+    prob = _problem(u, B, z, D, delta_bias, delta_softplus, dims)
+    args = _lib.S6BwdArgs()
+    args.p = prob
+    meta = lambda t: _strides(torch.empty_like(t, device="meta") if _dense(t)
+                              else torch.empty_like(u, dtype=t.dtype, device="meta"), 3)
+    args.u, args.u_stride = _ptr(u), _strides(u, 3)
+    args.delta, args.delta_stride = _ptr(delta), _strides(delta, 3)
+    args.dout, args.dout_stride = _ptr(dout), _strides(dout, 3)
+    args.z, args.z_stride = _ptr(z), _strides(z, 3)
+    args.out, args.out_stride = _ptr(out), _strides(out, 3)
+    # the outputs stand in as u's pointer (their layout and alignment enter the choice)
+    args.du, args.du_stride = _ptr(u), meta(u)
+    args.ddelta, args.ddelta_stride = _ptr(u), meta(delta)
+    if z is not None:
+        args.dz, args.dz_stride = _ptr(u), meta(z)
+        if recompute_out_z:
+            args.out_z, args.out_z_stride = _ptr(u), meta(z)
+    rc = _lib.LIB.s6_bwd_row_blocks(ctypes.byref(args))
+    if rc < 0:
+        _lib.check(rc, "s6_bwd_row_blocks")
+    return rc == 1
+
+
 def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, x_ckpt,
                             out=None, cu_seqlens=None, kernel_events=None, du_out=None,
                             dz_out=None, recompute_out_z=False):

@@ -334,6 +334,40 @@ def test_forward_row_block_choice(monkeypatch):
     assert q(fwd_args(batch=32, dim=256, seqlen=4096)) == 0    # the single-pass kernel
 
 
+def test_backward_row_block_choice(monkeypatch):
+    """s6_bwd_row_blocks: the backward's row blocks need every per-channel tensor it reads
+    and writes L-contiguous and 16-byte aligned, seqlen a multiple of 8 and dstate <= 16;
+    S6_BWD_ROWVEC=0 turns them off.  Host-only (fake pointers)."""
+    monkeypatch.delenv("S6_BWD_ROWVEC", raising=False)
+
+    def args(L=1024, N=16, z=0):
+        a = _lib.S6BwdArgs()
+        a.p = prob(seqlen=L, dstate=N, has_z=z)
+        rows = ("u", "delta", "dout", "du", "ddelta") + (("z", "out", "dz") if z else ())
+        for f in rows:
+            setattr(a, f, 0x10000)
+            setattr(a, f + "_stride", (a.p.dim * L, L, 1))
+        return a
+
+    q = lambda a: _lib.LIB.s6_bwd_row_blocks(ctypes.byref(a))
+    assert q(args()) == 1
+    assert q(args(z=1)) == 1
+    assert q(args(L=1004)) == 0
+    assert q(args(N=24)) == 0                                   # state groups of 16
+    a = args(z=1)
+    a.dz_stride = (a.p.dim * 1024, 1, a.p.dim)                  # a channel-last output
+    assert q(a) == 0
+    a = args(z=1)
+    a.out_z, a.out_z_stride = 0x10008, a.u_stride               # out_z 8-byte aligned only
+    assert q(a) == 0
+    a = args()
+    a.ddelta = 0x10004
+    assert q(a) == 0
+    monkeypatch.setenv("S6_BWD_ROWVEC", "0")
+    assert q(args()) == 0
+    assert q(args(L=0)) == _lib.E_INVALID
+
+
 def _ssd_problem(P=64, N=32, Q=64, z=0, L=300, H=4, G=2, batch=2):
     return _lib.S6SsdProblem(batch, L, H, P, G, N, Q, _lib.BF16, 1, 0, z, 1, 1, 0, 0, 0.0,
                              float("inf"))

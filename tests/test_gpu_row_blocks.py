@@ -77,3 +77,55 @@ def test_channel_last_and_unaligned_take_per_step_form(monkeypatch):
     big = torch.empty(2, 128, 1028, dtype=torch.bfloat16, device=DEV)
     xs = big[:, :, 2:1026]                         # rows start 4 bytes past 16-byte alignment
     assert not forward_row_blocks(xs, xc, A, Bm, Cm, D=D)
+
+
+BWD_CASES = [
+    # B, L, D, N, dtype, z, bias, cu_seqlens, recompute_out_z
+    (2, 1024, 128, 16, torch.bfloat16, False, False, None, False),
+    (2, 1000, 96, 16, torch.float32, True, True, None, False),
+    (1, 2048, 200, 8, torch.float16, True, False, None, True),
+    (2, 512, 64, 16, torch.bfloat16, True, True, None, True),
+    (2, 4096, 192, 16, torch.bfloat16, False, True, None, False),
+    (1, 3000, 128, 16, torch.bfloat16, False, True, [0, 3, 700, 701, 2999, 3000], False),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: "-".join(map(str, c[:7])).replace("torch.", ""))
+def test_backward_row_blocks_bit_identical_to_per_step(case, monkeypatch):
+    """The backward on L-contiguous tensors: row blocks against per-step accesses
+    (S6_BWD_ROWVEC=0) on the same forward outputs, every gradient bit for bit."""
+    from s6scan.selective_scan_interface import backward_row_blocks, selective_scan_backward
+
+    B, L, D, N, dtype, z, bias, cu, oz = case
+    inp = gen(B, L, D, N, dtype, seed=L + 2 * N, z=z, bias=bias)
+    monkeypatch.delenv("S6_BWD_ROWVEC", raising=False)
+    lc = lambda t: views(t.to(DEV), "contiguous") if t is not None else None
+    x, dl, zz, dy = lc(inp["x"]), lc(inp["delta"]), lc(inp["z"]), lc(inp["dy"])
+    Bm, Cm = bc_views(inp["B"].to(DEV), 1, "contiguous"), bc_views(inp["C"].to(DEV), 1, "contiguous")
+    A, Dv = inp["A"].to(DEV), inp["D"].to(DEV)
+    bb = inp["bias"].to(DEV) if inp["bias"] is not None else None
+    cu = torch.tensor(cu, dtype=torch.int32, device=DEV) if cu is not None else None
+    sp = inp["softplus"]
+    out, _, xck, _ = selective_scan_forward(x, dl, A, Bm, Cm, D=Dv, z=zz, delta_bias=bb,
+                                            delta_softplus=sp, cu_seqlens=cu, want_ckpt=True)
+    bwd = lambda: selective_scan_backward(x, dl, A, Bm, Cm, Dv, zz, bb, sp, dy, xck,
+                                          out=out if z else None, cu_seqlens=cu,
+                                          recompute_out_z=oz)
+    q = lambda: backward_row_blocks(x, dl, A, Bm, Cm, Dv, zz, bb, sp, dy,
+                                    out=out if z else None, cu_seqlens=cu, recompute_out_z=oz)
+    assert q(), "expected the row-block backward for this layout"
+    print(f"case {case}: row blocks", flush=True)
+    got = bwd()
+    torch.cuda.synchronize()
+    monkeypatch.setenv("S6_BWD_ROWVEC", "0")
+    assert not q()
+    print(f"case {case}: per step", flush=True)
+    ref = bwd()
+    torch.cuda.synchronize()
+    names = ("du", "ddelta", "dA", "dB", "dC", "dD", "dz", "ddelta_bias", "out_z")
+    assert len(got) == len(ref)
+    for name, a, b in zip(names, got, ref):
+        if b is None:
+            assert a is None, name
+            continue
+        assert torch.equal(a, b), f"{name}: max |diff| {(a.float() - b.float()).abs().max().item():.3g}"
