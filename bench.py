@@ -666,14 +666,15 @@ def measure_scan(torch, workload, steps, warmup, layout="channel_last"):
     # Dominant kernel: the scan/output pass of the forward (backward main kernel for the
     # fwd+bwd workloads); one launch processes every (token, channel) of the call.
     g0_ = sets[0]
-    from s6scan.selective_scan_interface import _problem, check_inputs
+    from s6scan.selective_scan_interface import forward_kernel
     z0 = g0_["z"].mT if mixer else None
-    dims = check_inputs(g0_["x"].mT, g0_["delta"].mT, g0_["A"], g0_["B"].mT, g0_["C"].mT,
-                        g0_["D"], z0, None, g0_.get("cu_seqlens"))
-    prob = _problem(g0_["x"].mT, g0_["B"].mT, z0, g0_["D"], None, mixer, dims)
-    single_pass = _lib.LIB.s6_fwd_single_pass(ctypes.byref(prob)) == 1
-    fwd_kernel = ("fwd_lanes (single-pass forward)" if single_pass
-                  else "fwd_scan (output pass of the chunked forward)")
+    d0 = g0_["dt_raw"] if mixer else g0_["delta"]
+    kind = forward_kernel(g0_["x"].mT, d0.mT, g0_["A"], g0_["B"].mT, g0_["C"].mT,
+                          g0_["D"], z0, None, mixer, g0_.get("cu_seqlens"))
+    fwd_kernel = {"single_pass": "fwd_lanes (single-pass forward)",
+                  "chunked": "fwd_scan (output pass of the chunked forward)",
+                  "chunked_rows": "fwd_scan (output pass of the chunked forward, 8-step row "
+                                  "blocks)"}[kind]
     if cfg.backward:
         dom_name, dom_ms, dom_bytes = "bwd_scan", kb_ms, nbytes - fwd_bytes
     else:

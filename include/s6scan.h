@@ -162,18 +162,28 @@ int s6_validate_cu_seqlens(const int32_t* cu_host, int64_t nseq, int64_t seqlen)
  * timing or profiling. */
 int s6_fwd_single_pass(const S6Problem* p);
 
-/* Host-only: 1 if the chunked forward moves these arguments' u / delta / z / out / out_z in
- * whole blocks of 8 steps per lane (16-byte accesses: each of those tensors has a contiguous
- * time axis, 16-byte aligned rows and blocks, seqlen is a multiple of 8 and dstate <= 32),
- * 0 if one step at a time (any strides) or on the single-pass kernel, or a negative code for
- * invalid arguments (the workspace is not checked).  Follows the environment override
- * S6_FWD_ROWVEC=0 (per-step accesses) as s6_fwd does.  Both give bit-identical results.  No
- * counterpart in the reference: it names the kernel variant a caller is timing. */
-int s6_fwd_row_blocks(const S6FwdArgs* a);
+/* Host-only: which forward kernels s6_fwd runs for these arguments, or a negative code for
+ * invalid arguments (the workspace is not checked):
+ *   S6_FWD_SINGLE_PASS   the single-pass kernel (as s6_fwd_single_pass says from the problem
+ *                        alone; arguments whose u / delta / out (z / out_z) have a contiguous
+ *                        time axis also take it with the z gate and at any wave count);
+ *   S6_FWD_CHUNKED_ROWS  the chunked kernels moving u / delta / z / out / out_z in whole
+ *                        8-step row blocks per lane (those tensors L-contiguous with 16-byte
+ *                        aligned rows and blocks, seqlen a multiple of 8, dstate <= 32);
+ *   S6_FWD_CHUNKED       the chunked kernels, one step at a time (any strides).
+ * Follows the environment overrides S6_FWD_PATH=lanes / chunked and S6_FWD_ROWVEC=0 (per-step
+ * accesses) as s6_fwd does; the two chunked forms give bit-identical results.  No
+ * counterpart in the reference: it names the kernels a caller is timing. */
+#define S6_FWD_CHUNKED 0
+#define S6_FWD_CHUNKED_ROWS 1
+#define S6_FWD_SINGLE_PASS 2
+int s6_fwd_kernel(const S6FwdArgs* a);
 
-/* Host-only: the same for s6_bwd (u, delta, dout, du, ddelta and, with z, z, out, dz and
- * out_z when given; dstate <= 16; override S6_BWD_ROWVEC=0).  Checks the problem only, not
- * the other arguments.  No counterpart in the reference. */
+/* Host-only: 1 if s6_bwd moves u, delta, dout, du, ddelta (with z: z, out, dz and out_z when
+ * given) in whole 8-step row blocks per lane (each L-contiguous with 16-byte aligned rows and
+ * blocks, seqlen a multiple of 8, dstate <= 16), 0 if one step at a time, or a negative code
+ * for an invalid problem (the other arguments are not checked).  Override S6_BWD_ROWVEC=0;
+ * both forms give bit-identical results.  No counterpart in the reference. */
 int s6_bwd_row_blocks(const S6BwdArgs* a);
 
 /* Number of x_ckpt entries along the sequence: ceil(seqlen / S6_CKPT_INTERVAL). */

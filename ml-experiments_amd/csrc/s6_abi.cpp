@@ -135,10 +135,15 @@ constexpr int64_t kLanesMinWaves = 2048;
 int64_t lanes_ns(int64_t N) { return N <= 16 ? 16 : N <= 32 ? 32 : 64; }
 int64_t lanes_cpg(int64_t N) { return 4 * (64 / lanes_ns(N)); }  // channels per workgroup
 
-bool choose_lanes(const S6Problem& p) {
+bool lanes_eligible(const S6Problem& p) {
   if (p.nseq > 0 || p.dstate < 9 || p.dstate > 64) return false;
   const char* env = getenv("S6_FWD_PATH");
-  if (env != nullptr && strcmp(env, "chunked") == 0) return false;
+  return env == nullptr || strcmp(env, "chunked") != 0;
+}
+
+bool choose_lanes(const S6Problem& p) {
+  if (!lanes_eligible(p)) return false;
+  const char* env = getenv("S6_FWD_PATH");
   if (env != nullptr && strcmp(env, "lanes") == 0) return true;
   if (p.has_z) return false;
   const int64_t Dg = p.dim / p.ngroups;
@@ -146,12 +151,28 @@ bool choose_lanes(const S6Problem& p) {
   return waves >= kLanesMinWaves;
 }
 
+// u / delta / out (z / out_z) with a contiguous time axis, the [B, D, L] layout zoology's
+// Mamba passes.  There the chunked kernels, one lane per channel, touch one cache line per
+// lane at every access and re-fetch each line for every block of it they use (5-8x the
+// algorithmic bytes measured), while the single-pass kernel's 16 lanes of a channel read 16
+// consecutive steps together.  Measured on such inputs (same box, forward time):
+//   B32 L4096 D256 N16 bf16, softplus + bias + z gate: chunked 0.555 -> single-pass 0.263 ms
+//   B8 L8192 D768 N16 bf16 with checkpoints (1536 waves): 0.669 -> 0.406 ms
+// so every single-pass-eligible problem takes it on this layout, whatever the wave count and
+// the z gate.  This only ever adds single-pass choices, which need no workspace: sizing from
+// the problem alone stays an upper bound.
+bool lcontig_rows(const S6FwdArgs& a) {
+  bool ok = a.u_stride[2] == 1 && a.delta_stride[2] == 1 && a.out_stride[2] == 1;
+  if (a.p.has_z) ok = ok && a.z_stride[2] == 1 && a.out_z_stride[2] == 1;
+  return ok;
+}
+
 // Chunking and workspace layout; ptrs may be null (sizing only, then relayout is assumed
-// to be needed).
+// to be needed).  lcontig: the forward's per-channel tensors are L-contiguous (lcontig_rows).
 Plan make_plan(const S6Problem& p, bool bwd, const void* Bp, const int64_t* sB, const void* Cp,
-               const int64_t* sC) {
+               const int64_t* sC, bool lcontig = false) {
   Plan pl{};
-  if (!bwd && choose_lanes(p)) {
+  if (!bwd && (choose_lanes(p) || (lcontig && lanes_eligible(p)))) {
     pl.lanes = true;
     pl.Dg = p.dim / p.ngroups;
     pl.nJ = ceil_div(pl.Dg, lanes_cpg(p.dstate));
@@ -300,6 +321,11 @@ bool choose_rowvec(const S6FwdArgs& a, const Plan& pl) {
             rows_vec_ok(a.out, a.out_stride, es, p);
   if (p.has_z) ok = ok && rows_vec_ok(a.z, a.z_stride, es, p) && rows_vec_ok(a.out_z, a.out_z_stride, es, p);
   return ok;
+}
+
+// The forward's plan for these arguments (their layout can select the single-pass kernel).
+Plan fwd_plan(const S6FwdArgs& a) {
+  return make_plan(a.p, false, a.B, a.B_stride, a.C, a.C_stride, lcontig_rows(a));
 }
 
 // The backward's row blocks (one wave per 64-channel block, dstate <= 16): every per-channel
@@ -1106,11 +1132,12 @@ int s6_bwd_row_blocks(const S6BwdArgs* a) {
   return choose_rowvec_bwd(*a) ? 1 : 0;
 }
 
-int s6_fwd_row_blocks(const S6FwdArgs* a) {
+int s6_fwd_kernel(const S6FwdArgs* a) {
   int r = validate_fwd(a, false);
   if (r != S6_OK) return r;
-  const Plan pl = make_plan(a->p, false, a->B, a->B_stride, a->C, a->C_stride);
-  return choose_rowvec(*a, pl) ? 1 : 0;
+  const Plan pl = fwd_plan(*a);
+  if (pl.lanes) return S6_FWD_SINGLE_PASS;
+  return choose_rowvec(*a, pl) ? S6_FWD_CHUNKED_ROWS : S6_FWD_CHUNKED;
 }
 
 }  // extern "C"
@@ -1130,7 +1157,7 @@ int validate_fwd(const S6FwdArgs* a, bool check_workspace) {
   if (p.has_z && ((r = check_ptr(a->out_z, "out_z")) || (r = check_strides(a->out_z_stride, 3, "out_z"))))
     return r;
   if (a->x_ckpt != nullptr && (r = check_ckpt(a->x_ckpt_stride))) return r;
-  const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
+  const Plan pl = fwd_plan(*a);
   const int es = esize(p.io_dtype);
   // (the single-pass kernel addresses its tensors with 64-bit indices)
   if (!pl.lanes &&
@@ -1200,7 +1227,7 @@ int s6_fwd(const S6FwdArgs* a, void* stream) {
 int s6_fwd_noalloc(const S6FwdArgs* a, void* stream) {
   int r = validate_fwd(a, false);
   if (r != S6_OK) return r;
-  const Plan pl = make_plan(a->p, false, a->B, a->B_stride, a->C, a->C_stride);
+  const Plan pl = fwd_plan(*a);
   if (pl.total_fwd > (size_t)S6_NOALLOC_SCRATCH_BYTES)
     return fail(S6_E_WORKSPACE,
                 "s6_fwd_noalloc: this problem needs %zu bytes of scratch, above the library's "
@@ -1222,7 +1249,7 @@ namespace {
 int run_fwd(const S6FwdArgs& args, hipStream_t st) {
   const S6FwdArgs* a = &args;
   const S6Problem& p = a->p;
-  const Plan pl = make_plan(p, false, a->B, a->B_stride, a->C, a->C_stride);
+  const Plan pl = fwd_plan(*a);
   char* ws = (char*)a->workspace;
   hipError_t e = hipSuccess;
   if (pl.relayout_B)

@@ -23,6 +23,7 @@ NOALLOC_SCRATCH_BYTES = 64 << 20
 
 F32, BF16, F16 = 0, 1, 2
 OK, E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_HIP = 0, -1, -2, -3, -4
+FWD_CHUNKED, FWD_CHUNKED_ROWS, FWD_SINGLE_PASS = 0, 1, 2  # s6_fwd_kernel
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libs6scan.so")
 
@@ -209,7 +210,7 @@ EXPORTS = {
     "s6_validate_bwd": (ctypes.c_int, [ctypes.POINTER(S6BwdArgs)]),
     "s6_validate_cu_seqlens": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]),
     "s6_fwd_single_pass": (ctypes.c_int, [ctypes.POINTER(S6Problem)]),
-    "s6_fwd_row_blocks": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs)]),
+    "s6_fwd_kernel": (ctypes.c_int, [ctypes.POINTER(S6FwdArgs)]),
     "s6_bwd_row_blocks": (ctypes.c_int, [ctypes.POINTER(S6BwdArgs)]),
     "s6_num_checkpoints": (ctypes.c_int64, [ctypes.POINTER(S6Problem)]),
     "s6_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(S6Problem)]),

@@ -201,11 +201,14 @@ def _fwd_args(prob, u, delta, A, B4, C4, D, z, delta_bias, cu_seqlens, out, out_
     return args
 
 
-def forward_row_blocks(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                       cu_seqlens=None):
-    """True if selective_scan_forward on these tensors (outputs laid out like u, as it
-    allocates them) runs the chunked kernels with whole 8-step row blocks per lane
-    (``s6_fwd_row_blocks``); False for per-step accesses or the single-pass kernel.  Host
+_FWD_KERNELS = {0: "chunked", 1: "chunked_rows", 2: "single_pass"}
+
+
+def forward_kernel(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                   cu_seqlens=None):
+    """The forward kernels selective_scan_forward runs on these tensors, outputs laid out like
+    u as it allocates them (``s6_fwd_kernel``): "single_pass", "chunked_rows" (the chunked
+    kernels with whole 8-step row blocks per lane) or "chunked" (one step at a time).  Host
     only: no kernel runs and nothing is allocated on the device."""
     dims = check_inputs(u, delta, A, B, C, D, z, delta_bias, cu_seqlens)
     prob = _problem(u, B, z, D, delta_bias, delta_softplus, dims)
@@ -217,10 +220,10 @@ def forward_row_blocks(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     args.out_stride = like
     if z is not None:
         args.out_z_stride = like
-    rc = _lib.LIB.s6_fwd_row_blocks(ctypes.byref(args))
+    rc = _lib.LIB.s6_fwd_kernel(ctypes.byref(args))
     if rc < 0:
-        _lib.check(rc, "s6_fwd_row_blocks")
-    return rc == 1
+        _lib.check(rc, "s6_fwd_kernel")
+    return _FWD_KERNELS[rc]
 
 
 def selective_scan_forward(u, delta, A, B, C, D=None, z=None, delta_bias=None,

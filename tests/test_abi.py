@@ -40,6 +40,9 @@ def test_header_constants_match_binding():
     assert int(consts["S6_CKPT_INTERVAL"]) == _lib.CKPT_INTERVAL
     assert int(consts["S6_MAX_DSTATE_FWD"]) == _lib.MAX_DSTATE_FWD
     assert int(consts["S6_MAX_DSTATE_BWD"]) == _lib.MAX_DSTATE_BWD
+    assert (int(consts["S6_FWD_CHUNKED"]), int(consts["S6_FWD_CHUNKED_ROWS"]),
+            int(consts["S6_FWD_SINGLE_PASS"])) == (_lib.FWD_CHUNKED, _lib.FWD_CHUNKED_ROWS,
+                                                   _lib.FWD_SINGLE_PASS)
 
 
 def prob(**kw):
@@ -108,7 +111,7 @@ def test_validate_fwd_ok_and_errors():
     a.u = None
     assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_INVALID
     assert "u must not be NULL" in _lib.last_error()
-    a = fwd_args()
+    a = fwd_args(dstate=8)  # the chunked forward (the single-pass one needs no workspace)
     a.workspace_bytes = 8
     assert _lib.LIB.s6_validate_fwd(ctypes.byref(a)) == _lib.E_WORKSPACE
     a = fwd_args()
@@ -298,40 +301,54 @@ def test_forward_kernel_choice(monkeypatch):
     assert q(batch=0) == _lib.E_INVALID
 
 
-def test_forward_row_block_choice(monkeypatch):
-    """s6_fwd_row_blocks says whether the chunked forward moves u / delta / z / out / out_z in
-    whole 8-step row blocks: only for a contiguous time axis with 16-byte aligned rows and
-    blocks, seqlen a multiple of 8, dstate <= 32 and not the single-pass kernel; the
-    environment override S6_FWD_ROWVEC=0 turns it off.  Host-only (fake pointers)."""
+def test_forward_kernel_for_arguments(monkeypatch):
+    """s6_fwd_kernel names the forward kernels for a call's arguments.  The chunked kernels
+    move u / delta / z / out / out_z in whole 8-step row blocks only for a contiguous time axis
+    with 16-byte aligned rows and blocks, seqlen a multiple of 8 and dstate <= 32; on an
+    L-contiguous layout every single-pass-eligible problem (dstate 9-64, no varlen) takes the
+    single-pass kernel, z gate and small wave counts included.  Overrides S6_FWD_ROWVEC=0 and
+    S6_FWD_PATH.  Host-only (fake pointers)."""
+    CH, ROWS, SP = _lib.FWD_CHUNKED, _lib.FWD_CHUNKED_ROWS, _lib.FWD_SINGLE_PASS
     monkeypatch.delenv("S6_FWD_ROWVEC", raising=False)
+    monkeypatch.delenv("S6_FWD_PATH", raising=False)
+    q = lambda a: _lib.LIB.s6_fwd_kernel(ctypes.byref(a))
+    assert q(fwd_args(seqlen=1024)) == SP                      # [B, D, L] L-contiguous
+    assert q(fwd_args(seqlen=1024, dstate=8)) == ROWS          # below the single-pass range
+    assert q(fwd_args(seqlen=1004, dstate=8)) == CH            # a partial last block
+    zl = fwd_args(seqlen=1024, has_z=1)
+    zl.z = zl.out_z = 0x20000
+    zl.z_stride = zl.out_z_stride = zl.u_stride
+    assert q(zl) == SP                                         # the z gate too, on this layout
+    cl = fwd_args(seqlen=1024)
+    cl.u_stride = cl.delta_stride = cl.out_stride = (cl.p.dim * 1024, 1, cl.p.dim)
+    assert q(cl) == CH                                         # channel-last, 16 waves
+    big = fwd_args(batch=32, dim=256, seqlen=4096)
+    big.u_stride = big.delta_stride = big.out_stride = (256 * 4096, 1, 256)
+    assert q(big) == SP                                        # channel-last, 2048 waves
     monkeypatch.setenv("S6_FWD_PATH", "chunked")
-    q = lambda a: _lib.LIB.s6_fwd_row_blocks(ctypes.byref(a))
-    assert q(fwd_args(seqlen=1024)) == 1                       # [B, D, L] L-contiguous
-    assert q(fwd_args(seqlen=1000)) == 1                       # 1000 = 125 blocks of 8
-    assert q(fwd_args(seqlen=1004)) == 0                       # a partial last block
-    assert q(fwd_args(seqlen=1024, dstate=32)) == 1
-    assert q(fwd_args(seqlen=1024, dstate=48)) == 0            # one wave per 16 states
+    assert q(fwd_args(seqlen=1024)) == ROWS
+    assert q(fwd_args(seqlen=1000)) == ROWS                    # 1000 = 125 blocks of 8
+    assert q(fwd_args(seqlen=1004)) == CH
+    assert q(fwd_args(seqlen=1024, dstate=32)) == ROWS
+    assert q(fwd_args(seqlen=1024, dstate=48)) == CH           # one wave per 16 states
     a = fwd_args(seqlen=1024)
-    a.u_stride = (a.p.dim * 1024, 1, a.p.dim)                  # channel-last view
-    assert q(a) == 0
+    a.u_stride = (a.p.dim * 1024, 1, a.p.dim)                  # one channel-last view
+    assert q(a) == CH
     a = fwd_args(seqlen=1024)
     a.out = 0x10000 + 8                                        # out rows 8-byte aligned only
-    assert q(a) == 0
+    assert q(a) == CH
     a = fwd_args(seqlen=1024, io_dtype=_lib.F32, bc_dtype=_lib.F32)
     a.delta_stride = (a.p.dim * 1026, 1026, 1)                 # rows 4104 B apart: not 16-aligned
-    assert q(a) == 0
+    assert q(a) == CH
     a = fwd_args(seqlen=1024, has_z=1)
     assert q(a) == _lib.E_INVALID                              # z / out_z missing
     a.z = a.out_z = 0x20000
     a.z_stride = a.out_z_stride = a.u_stride
-    assert q(a) == 1
+    assert q(a) == ROWS
     a.out_z_stride = (a.p.dim * 1024, 1, a.p.dim)
-    assert q(a) == 0
+    assert q(a) == CH
     monkeypatch.setenv("S6_FWD_ROWVEC", "0")
-    assert q(fwd_args(seqlen=1024)) == 0
-    monkeypatch.delenv("S6_FWD_ROWVEC")
-    monkeypatch.setenv("S6_FWD_PATH", "lanes")
-    assert q(fwd_args(batch=32, dim=256, seqlen=4096)) == 0    # the single-pass kernel
+    assert q(fwd_args(seqlen=1024)) == CH
 
 
 def test_backward_row_block_choice(monkeypatch):

@@ -3,13 +3,14 @@ time axis (the [B, D, L] layout of the reference's callers, mamba.py:128-132) an
 multiple of 8, each lane moves whole 8-step row blocks with 16-byte accesses; otherwise one
 step at a time.  The arithmetic is the same, so out, out_z, the checkpoints and the final
 states must be bit-identical between the two (S6_FWD_ROWVEC=0 forces per-step accesses on the
-same tensors), and ``forward_row_blocks`` must name the form that ran.  The per-step form is
+same tensors), and ``forward_kernel`` must name the form that ran (the single-pass kernel, which
+L-contiguous inputs otherwise get at these dstates, is switched off with S6_FWD_PATH=chunked).  The per-step form is
 held to the oracle by the parity tests; the row-block form is too, by the contiguous-layout
 cases there."""
 import pytest
 import torch
 
-from s6scan.selective_scan_interface import forward_row_blocks, selective_scan_forward
+from s6scan.selective_scan_interface import forward_kernel, selective_scan_forward
 from test_gpu_parity import bc_views, gen, views
 
 pytestmark = pytest.mark.gpu
@@ -36,7 +37,7 @@ def _run(inp, cu):
     bias = inp["bias"].to(DEV) if inp["bias"] is not None else None
     cu = torch.tensor(cu, dtype=torch.int32, device=DEV) if cu is not None else None
     kw = dict(D=D, z=z, delta_bias=bias, delta_softplus=inp["softplus"], cu_seqlens=cu)
-    rows = forward_row_blocks(x, dl, A, Bm, Cm, **kw)
+    rows = forward_kernel(x, dl, A, Bm, Cm, **kw) == "chunked_rows"
     res = selective_scan_forward(x, dl, A, Bm, Cm, **kw, want_ckpt=True, want_last_state=True)
     torch.cuda.synchronize()
     return rows, res
@@ -71,12 +72,12 @@ def test_channel_last_and_unaligned_take_per_step_form(monkeypatch):
     A, D = inp["A"].to(DEV), inp["D"].to(DEV)
     Bm, Cm = bc_views(inp["B"].to(DEV), 1, "view"), bc_views(inp["C"].to(DEV), 1, "view")
     x, dl = views(inp["x"].to(DEV), "view"), views(inp["delta"].to(DEV), "view")
-    assert not forward_row_blocks(x, dl, A, Bm, Cm, D=D)
+    assert forward_kernel(x, dl, A, Bm, Cm, D=D) == "chunked"
     xc = views(inp["x"].to(DEV), "contiguous")
-    assert forward_row_blocks(xc, xc, A, Bm, Cm, D=D)
+    assert forward_kernel(xc, xc, A, Bm, Cm, D=D) == "chunked_rows"
     big = torch.empty(2, 128, 1028, dtype=torch.bfloat16, device=DEV)
     xs = big[:, :, 2:1026]                         # rows start 4 bytes past 16-byte alignment
-    assert not forward_row_blocks(xs, xc, A, Bm, Cm, D=D)
+    assert forward_kernel(xs, xc, A, Bm, Cm, D=D) == "chunked"
 
 
 BWD_CASES = [
@@ -129,3 +130,21 @@ def test_backward_row_blocks_bit_identical_to_per_step(case, monkeypatch):
             assert a is None, name
             continue
         assert torch.equal(a, b), f"{name}: max |diff| {(a.float() - b.float()).abs().max().item():.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chunked_row_blocks_match_restatement(dtype, monkeypatch):
+    """The chunked row-block forward (forced: L-contiguous inputs at dstate 16 otherwise take
+    the single-pass kernel) against the oracle, z gate and softplus bias included; fp32 against
+    the float64 evaluation of the restatement (see test_forward_matches_restatement)."""
+    from test_gpu_parity import ref_fwd, ref_fwd64
+    from tolerances import assert_out_close, assert_state_close
+
+    monkeypatch.setenv("S6_FWD_PATH", "chunked")
+    monkeypatch.delenv("S6_FWD_ROWVEC", raising=False)
+    inp = gen(2, 1000, 128, 16, dtype, seed=21, z=True, bias=True)
+    rows, (out, out_z, _, ls) = _run(inp, None)
+    assert rows
+    ref, ref_ls = ref_fwd64(inp) if dtype == torch.float32 else ref_fwd(inp)
+    assert_out_close(out_z, ref, dtype, dstate=16)
+    assert_state_close(ls, ref_ls)
