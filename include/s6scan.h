@@ -157,7 +157,8 @@ int s6_validate_cu_seqlens(const int32_t* cu_host, int64_t nseq, int64_t seqlen)
 
 /* Host-only: 1 if s6_fwd runs this problem on the single-pass kernel (one lane per
  * (channel, state)), 0 if on the chunked kernels (chunk summaries, carry, output pass), or a
- * negative code for an invalid problem.  Follows the environment override S6_FWD_PATH=lanes /
+ * negative code for an invalid problem.  From the problem alone: arguments with L-contiguous
+ * u / delta / out (z / out_z) can also take the single-pass kernel (s6_fwd_kernel).  Follows the environment override S6_FWD_PATH=lanes /
  * chunked as s6_fwd does.  No counterpart in the reference: it names the kernel a caller is
  * timing or profiling. */
 int s6_fwd_single_pass(const S6Problem* p);
