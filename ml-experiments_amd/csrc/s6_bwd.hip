@@ -426,15 +426,18 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         for (int k = 0; k < HS; ++k) h[k] = hst[hh * HS + k];
 #pragma unroll
         for (int i = 0; i < SEG; ++i) {
+          // The B / C rotation runs at every step, past the end of a partial segment too
+          // (from clamped rows, unused there), so that no branch join has to merge the
+          // SGPR groups; only the arithmetic is per-step conditional.
+          bnx.touch();
+          const BCGroup<Tbc> bcur = bnx;
+          if (i + 1 < SEG) {
+            bnx.template load<HS>(Bbase + opaque((uint32_t)(min(ts + i + 1, te - 1) - t0) * Bst + hoff));
+          } else {  // first step of the reverse sweep
+            bnx.template load<HS>(Bbase + opaque((uint32_t)(te - 1 - t0) * Bst + hoff));
+            cnx.template load<HS>(Cbase + opaque((uint32_t)(te - 1 - t0) * Cst + hoff));
+          }
           if (ts + i < te) {
-            bnx.touch();
-            const BCGroup<Tbc> bcur = bnx;
-            if (ts + i + 1 < te) {
-              bnx.template load<HS>(Bbase + opaque((uint32_t)(ts + i + 1 - t0) * Bst + hoff));
-            } else {  // first step of the reverse sweep
-              bnx.template load<HS>(Bbase + opaque((uint32_t)(te - 1 - t0) * Bst + hoff));
-              cnx.template load<HS>(Cbase + opaque((uint32_t)(te - 1 - t0) * Cst + hoff));
-            }
             const float dtu = dt[i] * uu[i];
             auto body = [&](auto st_tag) {  // ST: a sequence starts at this step, h_{t-1} = 0
               constexpr bool ST = decltype(st_tag)::value;
@@ -492,18 +495,19 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
             p_hi = sa[((i - 2) * 2 + 1) * kWave + lane];
           }
         }
+        // As in the recompute, the rotation is unconditional (clamped rows past the end).
+        bnx.touch();
+        cnx.touch();
+        const BCGroup<Tbc> bcur = bnx, ccur = cnx;
+        if (i > 0) {
+          bnx.template load<HS>(Bbase + opaque((uint32_t)(min(t - 1, te - 1) - t0) * Bst + hoff));
+          cnx.template load<HS>(Cbase + opaque((uint32_t)(min(t - 1, te - 1) - t0) * Cst + hoff));
+        } else if (hh + 1 < NH) {  // next half, same segment
+          bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - t0) * Bst + hoff + HS * EB));
+        } else {  // first half of the previous segment (the first segment re-reads its own)
+          bnx.template load<HS>(Bbase + opaque((uint32_t)(max(ts - SEG, t0) - t0) * Bst));
+        }
         if (t < te) {
-          bnx.touch();
-          cnx.touch();
-          const BCGroup<Tbc> bcur = bnx, ccur = cnx;
-          if (i > 0) {
-            bnx.template load<HS>(Bbase + opaque((uint32_t)(t - 1 - t0) * Bst + hoff));
-            cnx.template load<HS>(Cbase + opaque((uint32_t)(t - 1 - t0) * Cst + hoff));
-          } else if (hh + 1 < NH) {  // next half, same segment
-            bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - t0) * Bst + hoff + HS * EB));
-          } else if (s > 0) {  // first half of the previous segment
-            bnx.template load<HS>(Bbase + opaque((uint32_t)(ts - SEG - t0) * Bst));
-          }
           // Without LDS_A, Delta passes through an empty asm so that exp(Delta A) is recomputed
           // here rather than kept live from the recompute above (64 more VGPRs per lane).
           float dti = dt[i];
