@@ -6,8 +6,9 @@
 // waves run the whole sequence in one pass with no chunk summaries, no carry kernel and no
 // second exp per element.  Per 16-step block:
 //   * the block's u, delta (and z) of the wave's channels are loaded once, lane i of a row
-//     holding step sigma(i); Delta = prep(delta) and Delta u are formed there, and each step
-//     reads them back through a DPP row broadcast folded into its multiplies;
+//     holding step sigma(i) (for [B, L, D] tensors the workgroup loads them channel-fastest
+//     and the lanes read them from LDS); Delta = prep(delta) and Delta u are formed there,
+//     and each step reads them back through a DPP row broadcast folded into its multiplies;
 //   * B_t and C_t of the block, shared by all channels of the workgroup (4 waves of the
 //     same batch and group), are staged in LDS as fp32 (B, C) pairs, double-buffered, one
 //     barrier per block;
@@ -145,7 +146,9 @@ template <> struct Raw<f16> {
 
 }  // namespace
 
-template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z>
+// CK: checkpoint stores (an x_ckpt tensor is given).  COOP: u / delta are loaded by the
+// workgroup and reach the lanes through LDS (see below); otherwise each lane loads its own.
+template <typename Tio, typename Tbc, int NS, int DTM, bool HAS_Z, bool CK, bool COOP>
 __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   constexpr int RPC = NS / 16;        // rows (of 16 lanes) per channel
   constexpr int PD = kPD<NS>;         // prefetch distance in blocks
@@ -153,7 +156,10 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   constexpr int CPG = 4 * CPW;        // channels per workgroup
   constexpr int NBC = kLT * NS / 256; // B/C elements staged per thread per block
   constexpr int ES = Elem<Tio>::kSize, EB = Elem<Tbc>::kSize;
+  constexpr int TE = kLT * CPG;       // u / delta elements of a block's workgroup tile
   __shared__ float2 bcs[2][kLT][NS];
+  __shared__ uint2 uds[COOP ? 2 : 1][COOP ? kLT : 1][CPG];  // raw (u, delta) bits, [step][channel]
+  __shared__ uint32_t zds[COOP && HAS_Z ? 2 : 1][COOP && HAS_Z ? kLT : 1][CPG];
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -191,14 +197,28 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   // Buffer addressing (s6_common.h): a wave-uniform base rebuilt per block and 32-bit lane
   // offsets; lanes given kOffDrop read zeros and drop their stores, so no store needs a
   // divergent branch inside the block.
-  const char* const ub = (const char*)p.u + (b * p.su[0] + d0 * p.su[1]) * ES;
-  const char* const db = (const char*)p.delta + (b * p.sdl[0] + d0 * p.sdl[1]) * ES;
-  const char* const zb = HAS_Z ? (const char*)p.z + (b * p.sz[0] + d0 * p.sz[1]) * ES : ub;
+  //
+  // u / delta (/ z) elements.  Without COOP, lane i of a row loads its channel's step
+  // sigma(i).  With COOP (channels contiguous, [B, L, D]) the workgroup loads its [kLT][CPG]
+  // tile one element per thread, consecutive threads on consecutive channels, so that a
+  // wave instruction covers 4 steps x 16 channels (4 cache lines instead of 16), and the
+  // lanes read their values back from LDS.  Tile channels past the group's last one read
+  // that channel, as the mirrored lanes above do.
+  const int ett = COOP ? tid / CPG : sg;                    // step within the block
+  const int ecc = COOP ? tid % CPG : 0;                     // channel within the tile
+  const int64_t ech = COOP ? min((int64_t)ecc, Dg - 1 - jb * CPG) : (int64_t)cre;
+  const int64_t eb0 = COOP ? g * Dg + jb * CPG : d0;         // channel that ech counts from
+  const bool has_el = !COOP || tid < TE;                    // wave-uniform
+  const char* const ub = (const char*)p.u + (b * p.su[0] + eb0 * p.su[1]) * ES;
+  const char* const db = (const char*)p.delta + (b * p.sdl[0] + eb0 * p.sdl[1]) * ES;
+  const char* const zb = HAS_Z ? (const char*)p.z + (b * p.sz[0] + eb0 * p.sz[1]) * ES : ub;
   char* const ob = (char*)p.out + (b * p.so[0] + d0 * p.so[1]) * ES;
   char* const ozb = HAS_Z ? (char*)p.out_z + (b * p.soz[0] + d0 * p.soz[1]) * ES : ob;
-  const uint32_t vu = (uint32_t)((cre * p.su[1] + sg * p.su[2]) * ES);
-  const uint32_t vd = (uint32_t)((cre * p.sdl[1] + sg * p.sdl[2]) * ES);
-  const uint32_t vz = HAS_Z ? (uint32_t)((cre * p.sz[1] + sg * p.sz[2]) * ES) : 0u;
+  const uint32_t vu = has_el ? (uint32_t)((ech * p.su[1] + ett * p.su[2]) * ES) : kOffDrop;
+  const uint32_t vd = has_el ? (uint32_t)((ech * p.sdl[1] + ett * p.sdl[2]) * ES) : kOffDrop;
+  const uint32_t vz =
+      (HAS_Z && has_el) ? (uint32_t)((ech * p.sz[1] + ett * p.sz[2]) * ES) : kOffDrop;
+  const int lch = w * CPW + cr;                // this lane's channel within the tile
   const bool store_y = active && (row % RPC) == 0;
   const uint32_t vo = store_y ? (uint32_t)((cr * p.so[1] + sg * p.so[2]) * ES) : kOffDrop;
   const uint32_t voz = (HAS_Z && store_y) ? (uint32_t)((cr * p.soz[1] + sg * p.soz[2]) * ES) : kOffDrop;
@@ -219,8 +239,9 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
     vb[m] = sn < N ? (uint32_t)((sn * p.sB[2] + tt * p.sB[3]) * EB) : kOffDrop;
     vc[m] = sn < N ? (uint32_t)((sn * p.sC[2] + tt * p.sC[3]) * EB) : kOffDrop;
   }
-  // Inputs of one block, loaded two blocks ahead of use: the B / C tile (committed to LDS
-  // at the end of the block before its own) and this lane's u / delta / z.
+  // Inputs of one block, loaded PD blocks ahead of use: this thread's elements of the B / C
+  // tile (and, with COOP, of the u / delta (/ z) tile), committed to LDS at the end of the
+  // block before their own, and without COOP this lane's u / delta / z.
   struct Pref {
     uint32_t b[NBC], c[NBC];
     uint32_t u, dl, z;
@@ -235,7 +256,7 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
       P.b[m] = Raw<Tbc>::load(rb, pick_off(out, vb[m]));
       P.c[m] = Raw<Tbc>::load(rc, pick_off(out, vc[m]));
     }
-    const bool out = tail && t0 + sg >= L;
+    const bool out = tail && t0 + ett >= L;
     P.u = Raw<Tio>::load(make_rsrc(ub + (int64_t)t0 * p.su[2] * ES), pick_off(out, vu));
     P.dl = Raw<Tio>::load(make_rsrc(db + (int64_t)t0 * p.sdl[2] * ES), pick_off(out, vd));
     P.z = HAS_Z ? Raw<Tio>::load(make_rsrc(zb + (int64_t)t0 * p.sz[2] * ES), pick_off(out, vz))
@@ -247,6 +268,11 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
       const int e = tid + 256 * m;
       bcs[buf][e / NS][e % NS] = make_float2(Raw<Tbc>::get(P.b[m]), Raw<Tbc>::get(P.c[m]));
     }
+    if constexpr (COOP)
+      if (has_el) {
+        uds[buf][ett][ecc] = make_uint2(P.u, P.dl);
+        if constexpr (HAS_Z) zds[buf][ett][ecc] = P.z;
+      }
   };
 
   // Checkpoint rows: without a checkpoint tensor the resource holds no records, so its
@@ -272,8 +298,16 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
     constexpr int BUF = PAR & 1;
     Pref& Pc = P[PAR];           // this block's inputs; reloaded for block + PD below
     Pref& Pn = P[(PAR + 1) % PD];  // the next block's (B / C committed at the end)
-    const float uu = Raw<Tio>::get(Pc.u), zz = HAS_Z ? Raw<Tio>::get(Pc.z) : 0.f;
-    const float dt = prep_dt<DTM>(Raw<Tio>::get(Pc.dl), bias);
+    uint32_t ru = Pc.u, rd = Pc.dl, rz = Pc.z;
+    if constexpr (COOP) {
+      const uint2 ud = uds[BUF][sg][lch];
+      ru = ud.x;
+      rd = ud.y;
+      if constexpr (HAS_Z) rz = zds[BUF][sg][lch];
+    }
+    const float uu = Raw<Tio>::get(ru);
+    const float zz = HAS_Z ? Raw<Tio>::get(rz) : 0.f;
+    const float dt = prep_dt<DTM>(Raw<Tio>::get(rd), bias);
     const float dtu = dt * uu;
     issue(Pc, t0 + PD * kLT);
     // Phase 1: the block's B / C pairs from LDS, then everything that does not depend on
@@ -305,8 +339,9 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
       h = fmaf(a[j], h, bx[j]);
       pr[j] = bc[j].y * h;
       constexpr bool at_ck = (j & (kCk - 1)) == kCk - 1;
-      if (FULL ? at_ck : (at_ck || t == L - 1))
-        Buf<float>::store(rck, vck, (uint32_t)(j / kCk) * ck_step, h);
+      if constexpr (CK)
+        if (FULL ? at_ck : (at_ck || t == L - 1))
+          Buf<float>::store(rck, vck, (uint32_t)(j / kCk) * ck_step, h);
     });
     // Phase 3: y of step sigma(li), D u, gate, store.
     float y = row_transpose_reduce16(pr, li);
@@ -344,10 +379,23 @@ static hipError_t launch_lanes_z(const FwdK& k, hipStream_t st, void* const* ev)
   hipError_t e = record_event(ev, 0, st);
   if (e != hipSuccess) return e;
   const dim3 grid((unsigned)(k.Bsz * k.nDblk));
-  if (k.has_z)
-    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, true>), grid, dim3(256), 0, st, k);
+  // Workgroup-loaded u / delta pay where channels are contiguous (B32 L4096 D256 N16 bf16
+  // [B, L, D]: 222 -> 211 us; fp32 B16 L16384 D256 N64: 1.71 -> 1.47 ms) and cost where
+  // steps are ([B, D, L]: 209 -> 224 us, the z-gated 257 -> 278 us), so [B, D, L] and the
+  // z gate keep the per-lane loads.
+  const bool ck = k.x_ckpt != nullptr, coop = k.su[1] == 1 && !k.has_z;
+  if (k.has_z && ck)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, true, true, false>), grid, dim3(256), 0, st, k);
+  else if (k.has_z)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, true, false, false>), grid, dim3(256), 0, st, k);
+  else if (ck && coop)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false, true, true>), grid, dim3(256), 0, st, k);
+  else if (ck)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false, true, false>), grid, dim3(256), 0, st, k);
+  else if (coop)
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false, false, true>), grid, dim3(256), 0, st, k);
   else
-    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false>), grid, dim3(256), 0, st, k);
+    hipLaunchKernelGGL((fwd_lanes<Tio, Tbc, NS, DTM, false, false, false>), grid, dim3(256), 0, st, k);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return record_event(ev, 1, st);
 }
