@@ -158,8 +158,10 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   constexpr int ES = Elem<Tio>::kSize, EB = Elem<Tbc>::kSize;
   constexpr int TE = kLT * CPG;       // u / delta elements of a block's workgroup tile
   __shared__ float2 bcs[2][kLT][NS];
-  __shared__ uint2 uds[COOP ? 2 : 1][COOP ? kLT : 1][CPG];  // raw (u, delta) bits, [step][channel]
-  __shared__ uint32_t zds[COOP && HAS_Z ? 2 : 1][COOP && HAS_Z ? kLT : 1][CPG];
+  // raw (u, delta) bits, [step][channel]; the padded rows put the 16 steps a lane row reads
+  // in distinct banks
+  __shared__ uint2 uds[COOP ? 2 : 1][COOP ? kLT : 1][CPG + 1];
+  __shared__ uint32_t zds[COOP && HAS_Z ? 2 : 1][COOP && HAS_Z ? kLT : 1][CPG + 1];
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
