@@ -22,7 +22,11 @@ UNITS = [("s6_abi.cpp", "s6_abi", []), ("s6_misc.hip", "s6_misc", []),
          ("s6_conv.hip", "s6_conv", []), ("s6_ssu.hip", "s6_ssu", []),
          ("s6_ssd.hip", "s6_ssd", []), ("s6_ssd_bwd.hip", "s6_ssd_bwd", [])]
 UNITS += [(f"s6_{d}.hip", f"s6_{d}_{t}", [f"-DS6_TIO={ty}"])
-          for d in ("fwd", "bwd", "fwd_lanes") for t, ty in _TIO.items()]
+          for d in ("fwd", "bwd") for t, ty in _TIO.items()]
+# The single-pass forward is split further, per state count and B/C dtype.
+UNITS += [("s6_fwd_lanes.hip", f"s6_fwd_lanes_{t}_n{ns}_bc{bcf}",
+           [f"-DS6_TIO={ty}", f"-DS6_LANES_NS={ns}", f"-DS6_LANES_BCF32={bcf}"])
+          for t, ty in _TIO.items() for ns in (16, 32, 64) for bcf in (0, 1)]
 # The chunked forward's and the backward's row-block kernels (S6_FWD_VEC=1, S6_BWD_VEC=1)
 # are a second unit per dtype each.
 UNITS += [("s6_fwd.hip", f"s6_fwd_vec_{t}", [f"-DS6_TIO={ty}", "-DS6_FWD_VEC=1"])

@@ -411,19 +411,45 @@ static hipError_t launch_lanes_dt(const FwdK& k, hipStream_t st, void* const* ev
   }
 }
 
-template <typename Tio, typename Tbc>
-static hipError_t launch_lanes_ns(const FwdK& k, hipStream_t st, void* const* ev) {
-  if (k.N <= 16) return launch_lanes_dt<Tio, Tbc, 16>(k, st, ev);
-  if (k.N <= 32) return launch_lanes_dt<Tio, Tbc, 32>(k, st, ev);
-  return launch_lanes_dt<Tio, Tbc, 64>(k, st, ev);
+// One (state count, B/C dtype) share of the kernels.  Each share is its own translation
+// unit (S6_LANES_NS, S6_LANES_BCF32), so that the build compiles them in parallel.
+template <typename Tio, bool BCF32, int NS>
+hipError_t launch_fwd_lanes_part(const FwdK& k, hipStream_t st, void* const* ev) {
+  return launch_lanes_dt<Tio, std::conditional_t<BCF32, float, Tio>, NS>(k, st, ev);
 }
+
+#if !defined(S6_LANES_NS) || !defined(S6_LANES_BCF32)
+#error "s6_fwd_lanes.hip is built once per S6_LANES_NS (16, 32, 64) and S6_LANES_BCF32 (0, 1)"
+#endif
+
+template hipError_t launch_fwd_lanes_part<S6_TIO, S6_LANES_BCF32, S6_LANES_NS>(const FwdK&, hipStream_t,
+                                                                             void* const*);
+
+#if S6_LANES_NS == 16 && S6_LANES_BCF32 == 0
+#define S6_LANES_EXTERN(BCF, NS)                                                              \
+  extern template hipError_t launch_fwd_lanes_part<S6_TIO, BCF, NS>(const FwdK&, hipStream_t, \
+                                                                    void* const*);
+S6_LANES_EXTERN(true, 16)
+S6_LANES_EXTERN(false, 32)
+S6_LANES_EXTERN(true, 32)
+S6_LANES_EXTERN(false, 64)
+S6_LANES_EXTERN(true, 64)
+#undef S6_LANES_EXTERN
 
 template <typename Tio>
 hipError_t launch_fwd_lanes_io(const FwdK& k, int bc_dtype, hipStream_t st, void* const* ev) {
-  if (bc_dtype == S6_F32) return launch_lanes_ns<Tio, float>(k, st, ev);
-  return launch_lanes_ns<Tio, Tio>(k, st, ev);
+  const bool f32 = bc_dtype == S6_F32;
+  if (k.N <= 16)
+    return f32 ? launch_fwd_lanes_part<Tio, true, 16>(k, st, ev)
+               : launch_fwd_lanes_part<Tio, false, 16>(k, st, ev);
+  if (k.N <= 32)
+    return f32 ? launch_fwd_lanes_part<Tio, true, 32>(k, st, ev)
+               : launch_fwd_lanes_part<Tio, false, 32>(k, st, ev);
+  return f32 ? launch_fwd_lanes_part<Tio, true, 64>(k, st, ev)
+             : launch_fwd_lanes_part<Tio, false, 64>(k, st, ev);
 }
 
 template hipError_t launch_fwd_lanes_io<S6_TIO>(const FwdK&, int, hipStream_t, void* const*);
+#endif
 
 }  // namespace s6
