@@ -24,6 +24,7 @@ or PyTorch fallback: inputs that are not on a ROCm device raise ``RuntimeError``
 reference's complex-A and time-invariant-B/C variants raise ``NotImplementedError``.
 """
 import ctypes
+import os
 
 import torch
 
@@ -373,21 +374,41 @@ def selective_scan_backward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
     return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 
+def _recompute_default():
+    """``S6_RECOMPUTE_STATES=1`` in the environment makes state recomputation the default
+    for callers that cannot pass ``recompute_states`` (code written for the reference's
+    signature)."""
+    return os.environ.get("S6_RECOMPUTE_STATES", "0") not in ("", "0")
+
+
 class SelectiveScanFn(torch.autograd.Function):
     """Autograd boundary with the reference's 10 positional inputs (SSI:19-79), plus an
-    optional 11th, ``cu_seqlens``, for packed variable-length input."""
+    optional 11th, ``cu_seqlens``, for packed variable-length input, and a 12th,
+    ``recompute_states``.
+
+    By default the forward keeps the fp32 state after every 8th step ([B, ceil(L/8), D, N],
+    8 bytes per (b, t, d) at N = 16) for the backward.  With ``recompute_states`` it keeps
+    none.  The tensors held from forward to backward are then the inputs alone, as with
+    the reference's kernel (whose ``x`` is [B, D, ceil(L/2048), 2N], SSI:45-50), and the
+    backward first reruns the forward to regenerate the checkpoints.  The gradients are the
+    same bit for bit; the price is one more forward per backward."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                return_last_state=False, cu_seqlens=None):
+                return_last_state=False, cu_seqlens=None, recompute_states=None):
         need_grad = any(ctx.needs_input_grad[:8])
+        recompute = _recompute_default() if recompute_states is None else bool(recompute_states)
         out, out_z, x_ckpt, last_state = selective_scan_forward(
             u, delta, A, B, C, D, z, delta_bias, delta_softplus, cu_seqlens=cu_seqlens,
-            want_ckpt=need_grad, want_last_state=bool(return_last_state))
+            want_ckpt=need_grad and not recompute, want_last_state=bool(return_last_state))
         ctx.delta_softplus = delta_softplus
         ctx.has_z = z is not None
+        ctx.recompute = need_grad and recompute
+        if ctx.recompute:
+            x_ckpt = None
         ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, x_ckpt,
-                              out if z is not None else None, cu_seqlens)
+                              out if (z is not None and not ctx.recompute) else None,
+                              cu_seqlens)
         res = out_z if z is not None else out
         if return_last_state:
             ctx.mark_non_differentiable(last_state)
@@ -397,17 +418,26 @@ class SelectiveScanFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, *args):
         u, delta, A, B, C, D, z, delta_bias, x_ckpt, out, cu_seqlens = ctx.saved_tensors
+        if ctx.recompute:
+            # the same forward launches as a checkpointing forward: identical checkpoints
+            out_r, _, x_ckpt, _ = selective_scan_forward(
+                u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, cu_seqlens=cu_seqlens,
+                want_ckpt=True)
+            out = out_r if z is not None else None
         if x_ckpt is None:
             raise RuntimeError("s6scan: backward called but no checkpoint was saved in forward")
         du, ddelta, dA, dB, dC, dD, dz, dbias = selective_scan_backward(
             u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, x_ckpt, out=out,
             cu_seqlens=cu_seqlens)
-        return (du, ddelta, dA, dB, dC, dD, dz, dbias, None, None, None)
+        return (du, ddelta, dA, dB, dC, dD, dz, dbias, None, None, None, None)
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                      return_last_state=False, *, cu_seqlens=None):
+                      return_last_state=False, *, cu_seqlens=None, recompute_states=None):
     """if return_last_state is True, returns (out, last_state); last_state has shape
-    (batch, dim, dstate) (or (nseq, dim, dstate) with cu_seqlens) and carries no gradient."""
+    (batch, dim, dstate) (or (nseq, dim, dstate) with cu_seqlens) and carries no gradient.
+    ``recompute_states``: keep no state checkpoints from forward to backward and rerun the
+    forward in the backward instead (``SelectiveScanFn``); None takes the
+    ``S6_RECOMPUTE_STATES`` environment default (off)."""
     return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
-                                 return_last_state, cu_seqlens)
+                                 return_last_state, cu_seqlens, recompute_states)

@@ -347,6 +347,66 @@ def test_autograd_contract():
     assert x.grad is not None and x.grad.shape == x.shape
 
 
+def _fwd_bwd(inp, layout, cu=None, **extra):
+    """Outputs and leaf gradients of selective_scan_fn + backward on the GPU."""
+    names = ["x", "delta", "A", "B", "C", "D", "z", "bias"]
+    leaves = {k: (inp[k].to(DEV).requires_grad_() if inp[k] is not None else None) for k in names}
+    args, kw = call(dict(inp, **leaves), layout, DEV)
+    kw["return_last_state"] = False
+    out = s6scan.selective_scan_fn(*args, **kw, cu_seqlens=None if cu is None else cu.to(DEV),
+                                   **extra)
+    out.backward(views(inp["dy"].to(DEV), layout))
+    return out.detach(), {k: v.grad for k, v in leaves.items() if v is not None}
+
+
+@pytest.mark.parametrize("shape,z,bias,layout,cu", [
+    ((2, 1000, 256, 16, torch.bfloat16), True, True, "view", None),
+    ((2, 1024, 128, 16, torch.float32), False, False, "contiguous", None),
+    ((1, 1000, 64, 16, torch.float32), True, True, "view", [0, 100, 101, 450, 1000]),
+    ((2, 300, 96, 24, torch.float16), False, True, "view", None),
+])
+def test_recompute_states_gives_identical_results(shape, z, bias, layout, cu, monkeypatch):
+    """recompute_states keeps no checkpoints from the forward and reruns it in the backward.
+    That rerun makes the same launches as a checkpointing forward, so outputs and gradients
+    equal the default mode's bit for bit, whether the mode is chosen by argument or by the
+    S6_RECOMPUTE_STATES environment default."""
+    B, L, D, N, dtype = shape
+    inp = gen(B, L, D, N, dtype, seed=L + D, z=z, bias=bias)
+    cu = None if cu is None else torch.tensor(cu, dtype=torch.int32)
+    out0, g0 = _fwd_bwd(inp, layout, cu)
+    out1, g1 = _fwd_bwd(inp, layout, cu, recompute_states=True)
+    monkeypatch.setenv("S6_RECOMPUTE_STATES", "1")
+    out2, g2 = _fwd_bwd(inp, layout, cu)
+    for out, g in ((out1, g1), (out2, g2)):
+        assert torch.equal(out, out0)
+        for k in g0:
+            assert torch.equal(g[k], g0[k]), k
+
+
+def test_recompute_states_holds_no_checkpoints():
+    """Between forward and backward the default mode holds the fp32 checkpoints
+    ([B, ceil(L/8), D, N]); recompute_states holds none of them."""
+    B, L, D, N = 2, 4096, 256, 16
+    inp = gen(B, L, D, N, torch.bfloat16, seed=5)
+    names = ["x", "delta", "A", "B", "C", "D"]
+    held = {}
+    for mode in (False, True):
+        leaves = {k: inp[k].to(DEV).requires_grad_() for k in names}
+        args, kw = call(dict(inp, **leaves), "view", DEV)
+        kw["return_last_state"] = False
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        out = s6scan.selective_scan_fn(*args, **kw, recompute_states=mode)
+        torch.cuda.synchronize()
+        held[mode] = torch.cuda.memory_allocated() - base - out.numel() * out.element_size()
+        out.backward(views(inp["dy"].to(DEV), "view"))
+        assert leaves["x"].grad is not None
+        del out, leaves, args, kw
+    ckpt_bytes = B * (-(-L // 8)) * D * N * 4
+    assert held[False] >= ckpt_bytes
+    assert held[True] < ckpt_bytes // 8
+
+
 # ------------------------------------------------------------------ workload sizes
 
 def _cfg_inputs(k, **kw):
