@@ -146,6 +146,35 @@ def test_layouts_give_identical_results(path, monkeypatch):
         assert torch.equal(out, res[0][0]) and torch.equal(ls, res[0][1])
 
 
+@pytest.mark.parametrize("L,D,N,dtype,bias", [
+    (200, 200, 16, torch.bfloat16, True),
+    (136, 75, 32, torch.float32, False),
+    (100, 38, 64, torch.float16, True),
+    (77, 16, 16, torch.float32, True),
+])
+def test_single_pass_workgroup_loads_match_lane_loads(L, D, N, dtype, bias, monkeypatch):
+    """On [B, L, D] tensors without a z gate, the single-pass forward loads u / delta per
+    workgroup and hands them to the lanes through LDS; on [B, D, L] tensors each lane loads
+    its own.  Both forms make the same arithmetic, so outputs, final states and the state
+    checkpoints the backward reads are bit-identical, including channel counts that leave the
+    last workgroup part-empty (D % 16 != 0) and every state count's tile shape; the outputs
+    also meet the restatement's bar."""
+    monkeypatch.setenv("S6_FWD_PATH", "lanes")
+    inp = gen(2, L, D, N, dtype, seed=L + D, bias=bias)
+    res = []
+    for layout in ("view", "contiguous"):
+        args, kw = call(inp, layout, DEV)
+        out, _, x_ckpt, ls = s6scan.selective_scan_forward(
+            *args, kw["D"], None, kw["delta_bias"], kw["delta_softplus"], want_ckpt=True,
+            want_last_state=True)
+        res.append((out.contiguous(), ls, x_ckpt))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+    out_ref, ls_ref = ref_fwd64(inp) if dtype == torch.float32 else ref_fwd(inp)
+    assert_out_close(res[0][0], out_ref, dtype, dstate=N)
+    assert_state_close(res[0][1], ls_ref)
+
+
 def test_forward_is_deterministic_and_linear_in_u():
     inp = gen(2, 500, 128, 16, torch.float32, seed=6)
     args, kw = call(inp, "view", DEV)
