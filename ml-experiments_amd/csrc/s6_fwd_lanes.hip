@@ -162,6 +162,12 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   // in distinct banks
   __shared__ uint2 uds[COOP ? 2 : 1][COOP ? kLT : 1][CPG + 1];
   __shared__ uint32_t zds[COOP && HAS_Z ? 2 : 1][COOP && HAS_Z ? kLT : 1][CPG + 1];
+  // YST: y is stored by the workgroup too (see below).  At 32 / 64 states only one of a
+  // channel's 2 / 4 rows stores, so the workgroup issues 2 / 4 times fewer store
+  // instructions: fp32 B16 L16384 D256 N64 1.445 -> 1.388 ms.  At 16 states the count is
+  // the same and the LDS round trip costs (B32 L4096 D256 N16 bf16: 201 -> 210 us).
+  constexpr bool YST = COOP && NS >= 32;
+  __shared__ float ys[YST ? 2 : 1][YST ? kLT : 1][CPG + 1];  // y of a block, [step][channel]
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -221,6 +227,18 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
   const uint32_t vz =
       (HAS_Z && has_el) ? (uint32_t)((ech * p.sz[1] + ett * p.sz[2]) * ES) : kOffDrop;
   const int lch = w * CPW + cr;                // this lane's channel within the tile
+  // With YST, y goes back the same way: the lanes put it in LDS, and after the block's
+  // barrier each thread stores its tile element, channel-fastest (one block later).
+  char* const obw = (char*)p.out + (b * p.so[0] + eb0 * p.so[1]) * ES;
+  const bool yel = has_el && (!COOP || jb * CPG + ecc < Dg);
+  const uint32_t vyo = yel ? (uint32_t)((ecc * p.so[1] + ett * p.so[2]) * ES) : kOffDrop;
+  // block from step tp, in buffer buf; `none` drops every store (the first block has no
+  // predecessor), `tail` those past the sequence end
+  auto store_tile = [&](int tp, int buf, bool none, bool tail) {
+    const float yv = ys[YST ? buf : 0][YST ? ett % kLT : 0][ecc];
+    Buf<Tio>::store(make_rsrc(obw + (int64_t)tp * p.so[2] * ES),
+                    pick_off(none || (tail && tp + ett >= L), vyo), 0, yv);
+  };
   const bool store_y = active && (row % RPC) == 0;
   const uint32_t vo = store_y ? (uint32_t)((cr * p.so[1] + sg * p.so[2]) * ES) : kOffDrop;
   const uint32_t voz = (HAS_Z && store_y) ? (uint32_t)((cr * p.soz[1] + sg * p.soz[2]) * ES) : kOffDrop;
@@ -351,7 +369,12 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
     if constexpr (RPC >= 4) y += __shfl_xor(y, 32);
     const bool yout = !FULL && t0 + sg >= L;
     y = fmaf(uu, Dv, y);
-    Buf<Tio>::store(make_rsrc(ob + (int64_t)t0 * p.so[2] * ES), FULL ? vo : pick_off(yout, vo), 0, y);
+    if constexpr (YST) {
+      store_tile(max(t0 - kLT, 0), BUF ^ 1, t0 == 0, false);
+      if ((row % RPC) == 0) ys[BUF][sg][lch] = y;
+    } else {
+      Buf<Tio>::store(make_rsrc(ob + (int64_t)t0 * p.so[2] * ES), FULL ? vo : pick_off(yout, vo), 0, y);
+    }
     if (HAS_Z)
       Buf<Tio>::store(make_rsrc(ozb + (int64_t)t0 * p.soz[2] * ES), FULL ? voz : pick_off(yout, voz),
                       0, y * zz * sigmoidf_(zz));
@@ -373,6 +396,7 @@ __global__ void __launch_bounds__(256) fwd_lanes(FwdK p) {
       t0 = L;
     }
   });
+  if constexpr (YST) store_tile((L - 1) / kLT * kLT, ((L - 1) / kLT) & 1, false, true);
   if (p.last_state != nullptr && store_state) p.last_state[(b * p.D + d) * p.N + s] = h;
 }
 
