@@ -206,6 +206,11 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         uc[i] = Buf<Tio>::from_raw(un[i]);
         dc[i] = Buf<Tio>::from_raw(dn[i]);
         zc[i] = (HAS_Z && !MULTI) ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+        // converted here, not where the steps use them: the raw registers then die before
+        // the next block's loads reuse them, instead of being copied at the loop's back edge
+        // (a copy that waits for those loads and for every store issued since)
+        asm volatile("" : "+v"(uc[i]), "+v"(dc[i]));
+        if constexpr (HAS_Z && !MULTI) asm volatile("" : "+v"(zc[i]));
       }
     }
     // MULTI output pass: u (and z) of the steps this wave finishes after the block,
@@ -223,11 +228,12 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
         }
       }
     }
-    // VEC: unconditional (the last block re-reads itself), so that the next block's rows are
-    // always a fresh load; a skipped load would merge the old value back in, and the compiler
-    // then copies the fresh one right after its load, which waits for it.
+    // Unconditional (the last block re-reads itself: VEC from a clamped block, the per-step
+    // form from steps clamped to t1 - 1), so that the next block's inputs are always a fresh
+    // load; a skipped load would merge the old value back in, and the compiler then copies
+    // the fresh one, which waits for it.
     if constexpr (VEC) fetch(min(tb + TB, t1 - TB));
-    else if (tb + TB < t1) fetch(tb + TB);
+    else fetch(tb + TB);
     // A sequence starts inside this block, or right after it (its predecessor's final
     // state is stored at the block's last step).
     const bool blk_has_start = varlen && sc.pending <= (int64_t)tb + TB;
