@@ -130,8 +130,12 @@ __global__ void __launch_bounds__(kWave) bwd_summary(BwdK p) {
         oc[i] = Buf<Tio>::from_raw(on[i]);
         dc[i] = Buf<Tio>::from_raw(dn[i]);
         zc[i] = HAS_Z ? Buf<Tio>::from_raw(zn[i]) : 0.f;
+        // converted here, so that the raw registers die before the next block's loads reuse
+        // them (no back-edge copy that waits for those loads)
+        asm volatile("" : "+v"(oc[i]), "+v"(dc[i]));
+        if constexpr (HAS_Z) asm volatile("" : "+v"(zc[i]));
       }
-      if (tb > t0) fetch(tb - TB);
+      fetch(max(tb - TB, t0));  // unconditional: the first block re-reads itself
     }
     const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, tb) : 0u;
     seen_start = seen_start || smask != 0u;
