@@ -412,8 +412,9 @@ __global__ void __launch_bounds__(MULTI ? 4 * kWave : kWave)
     }
 #pragma unroll
     for (int n = 0; n < NS; ++n) hst[n] = (ts > 0 && n < N) ? hn[n] : 0.f;
-    if constexpr (VEC) fetch(max(ts - SEG, t0));
-    else if (s > 0) fetch(ts - SEG);
+    // unconditional in both forms (the first segment re-reads itself), so that the next
+    // segment's registers are always a fresh load and need no back-edge copy
+    fetch(max(ts - SEG, t0));
     const uint32_t smask = varlen ? start_mask_rev(rc, p.cu, ts) : 0u;
     float s1[SEG], s2[SEG];
 #pragma unroll
