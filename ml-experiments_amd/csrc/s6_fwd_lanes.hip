@@ -64,36 +64,51 @@ __device__ inline float dpp_qxor2(float v) {
                                                                0x4E, 0xf, 0xf, true));
 }
 
-// Bank-masked DPP adds (a bank is 4 consecutive lanes of a row).  out = x[perm] + x on the
-// lanes of banks `MLO` and y[perm] + y on those of `MHI`, perm = row_mirror (lane i <-> 15 - i)
-// or row_half_mirror (i <-> 7 - i inside each half row): two VALU instructions where a
-// select-based exchange takes three.  Inline asm because the write masks must not be
-// merged away; the s_nop covers the VALU-write -> DPP-read distance for x and y.
-#define S6_MASKED_PAIR(CTRL, MLO, MHI)                                                    \
-  __device__ inline float masked_pair_##CTRL(float x, float y) {                          \
-    float out;                                                                            \
-    asm("s_nop 1\n\t"                                                                   \
-        "v_add_f32_dpp %0, %1, %1 " #CTRL " row_mask:0xf bank_mask:" #MLO "\n\t"         \
-        "v_add_f32_dpp %0, %2, %2 " #CTRL " row_mask:0xf bank_mask:" #MHI                 \
-        : "=&v"(out)                                                                      \
-        : "v"(x), "v"(y));                                                                \
-    return out;                                                                           \
-  }
-S6_MASKED_PAIR(row_mirror, 0x3, 0xc)
-S6_MASKED_PAIR(row_half_mirror, 0x5, 0xa)
-#undef S6_MASKED_PAIR
+// Bank-masked DPP adds (a bank is 4 consecutive lanes of a row).  A pair writes out =
+// x[perm] + x on the lanes of one bank set and y[perm] + y on the others, perm =
+// row_mirror (lane i <-> 15 - i) or row_half_mirror (i <-> 7 - i inside each half row):
+// two VALU instructions where a select-based exchange takes three.  Inline asm because the
+// write masks must not be merged away.  Each stage's pairs are one asm block, so a single
+// s_nop covers the VALU-write -> DPP-read distance for the inputs: the DPP reads inside a
+// block only read registers written before it.
 
 // Sum over the 16 lanes of each row of pr[j] (lane = state, j = step).  Returns, on lane i,
 // the sum for step sigma(i).  i is the lane's index inside its row.
 __device__ inline float row_transpose_reduce16(const float (&pr)[kLT], int i) {
   // lanes i and 15 - i: lanes 0-7 (banks 0, 1) keep steps 0-7, lanes 8-15 steps 8-15
   float q[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) q[j] = masked_pair_row_mirror(pr[j], pr[j + 8]);
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %8, %8 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %16, %16 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %1, %9, %9 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %1, %17, %17 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %2, %10, %10 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %18, %18 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %3, %11, %11 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %3, %19, %19 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %4, %12, %12 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %4, %20, %20 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %5, %13, %13 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %5, %21, %21 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %6, %14, %14 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %6, %22, %22 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %7, %15, %15 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %7, %23, %23 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]), "=&v"(q[7])
+      : "v"(pr[0]), "v"(pr[1]), "v"(pr[2]), "v"(pr[3]), "v"(pr[4]), "v"(pr[5]), "v"(pr[6]), "v"(pr[7]), "v"(pr[8]), "v"(pr[9]), "v"(pr[10]), "v"(pr[11]), "v"(pr[12]), "v"(pr[13]), "v"(pr[14]), "v"(pr[15]));
   // lanes i and 7 - i of each half row: banks 0 and 2 keep q0-3, banks 1 and 3 q4-7
   float r[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) r[j] = masked_pair_row_half_mirror(q[j], q[j + 4]);
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %8, %8 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %1, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %2, %6, %6 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %2, %10, %10 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %3, %7, %7 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %3, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]), "v"(q[4]), "v"(q[5]), "v"(q[6]), "v"(q[7]));
   // quad exchange over bit 0: even lanes keep r0, r1
   const bool b0 = (i & 1) != 0;
   float s2[2];
